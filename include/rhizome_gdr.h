@@ -1,0 +1,177 @@
+/*
+ * rhizome_gdr.h -- C ABI of the MI355X (gfx950) gated delta-rule library
+ * (librhizome_gdr.so).
+ *
+ * The op, for one head with state S (d_v x d_k, S[i][j] at i*d_k + j,
+ * i = value row, j = key column -- the reference layout of
+ * crates/ops/src/delta.rs:63):
+ *
+ *     S_t = alpha_t * S_{t-1} * (I - beta_t k_t k_t^T) + beta_t v_t k_t^T
+ *     o_t = S_t q_t
+ *
+ * Every entry point takes plain pointers and sizes, validates everything it
+ * can before touching the GPU, never aborts, and returns an rhz_status.
+ * Device pointers are caller-owned device memory; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  Launches are
+ * asynchronous with respect to the host and stream-ordered.  No entry point
+ * allocates device memory: scratch space comes from the caller-provided
+ * workspace (size from the matching *_workspace_size query), so the buffers
+ * can live at offsets inside a planner arena (crates/plan/src/arena.rs:71,
+ * 256-byte aligned).  Results are deterministic (no atomics in any
+ * reduction) and batch-invariant: a sequence's outputs do not depend on the
+ * other sequences packed with it.
+ *
+ * Tensor layouts (row-major, dense or packed):
+ *   q, k          [tokens, H, d_k]
+ *   v, o          [tokens, H, d_v]
+ *   gate, beta    [tokens, H]          fp32
+ *   states        [seqs, H, d_v, d_k]  fp32
+ * Dense batches are the packed layout with tokens = B*T and sequence b at
+ * tokens [b*T, (b+1)*T).
+ */
+#ifndef RHIZOME_GDR_H
+#define RHIZOME_GDR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RHZ_GDR_ABI_VERSION 1
+
+/* Status codes.  The Rust wrapper maps INVALID_ARG to
+ * rhizome_core::Error::Shape and UNSUPPORTED / WORKSPACE to Error::Invalid
+ * (crates/core/src/error.rs:7-28). */
+typedef enum rhz_status {
+    RHZ_OK = 0,
+    RHZ_ERR_INVALID_ARG = 1, /* null pointer, bad dimension or size, bad enum */
+    RHZ_ERR_UNSUPPORTED = 2, /* well-formed but not supported (dims, dtype, algo) */
+    RHZ_ERR_WORKSPACE = 3,   /* workspace missing, too small or misaligned */
+    RHZ_ERR_HIP = 4          /* the HIP runtime reported an error */
+} rhz_status;
+
+/* RHZ_F64 is accepted only as the output dtype of rhz_philox_fill. */
+typedef enum rhz_dtype { RHZ_F32 = 0, RHZ_BF16 = 1, RHZ_F64 = 2 } rhz_dtype;
+
+/* What `gate` holds: the log-decay g_t = ln(alpha_t) (<= 0), or alpha_t in
+ * [0, 1] itself.  alpha_t = 0 forgets the past exactly (delta.rs:348-358). */
+typedef enum rhz_gate { RHZ_GATE_LOG_ALPHA = 0, RHZ_GATE_ALPHA = 1 } rhz_gate;
+
+/* Prefill algorithm.  AUTO picks CHUNKED for bf16 and RECURRENT for fp32.
+ * RECURRENT: token-sequential fp32 recurrence (the fp32-input path).
+ * CHUNKED:   64-token chunks, WY/UT transform, bf16 MFMA with fp32
+ *            accumulation and fp32 state (bf16 inputs only). */
+typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUNKED = 2 } rhz_algo;
+
+/* Op identities for rhz_gdr_query_support, named after the plan-level ops
+ * OpKind::DeltaScan / OpKind::DeltaStep (crates/plan/src/graph.rs:56-59). */
+typedef enum rhz_op {
+    RHZ_OP_DELTA_SCAN = 0, /* "gated_delta_scan_chunked" (graph.rs:124) */
+    RHZ_OP_DELTA_STEP = 1  /* "gated_delta_step" (graph.rs:125) */
+} rhz_op;
+
+/* Prefill over a dense batch or a packed variable-length batch.
+ * Replaces, batched over sequences and heads and with a rectangular state,
+ * gated_delta_sequential (delta.rs:133-154) and gated_delta_scan_chunked
+ * (delta.rs:159-197).  Unlike those two, initial_state is honoured (they
+ * reset S at t = 0); pass initial_state = NULL for their behaviour. */
+typedef struct rhz_gdr_prefill_args {
+    int32_t batch;   /* dense: B;  packed: number of sequences N (>= 1) */
+    int32_t seq_len; /* dense: T;  packed: total tokens in the pack (>= 0) */
+    int32_t heads;   /* H >= 1 */
+    int32_t d_k;     /* 1..256 (RECURRENT), 1..128 (CHUNKED) */
+    int32_t d_v;     /* 1..1024 */
+    int32_t chunk;   /* requested chunk length >= 1; the result does not depend on it
+                        (delta.rs:156-157); CHUNKED computes with 64 */
+    int32_t dtype;     /* rhz_dtype of q, k, v and o */
+    int32_t gate_kind; /* rhz_gate */
+    int32_t algo;      /* rhz_algo */
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* gate;
+    const float* beta;
+    const int32_t* cu_seqlens;  /* device [N+1] non-decreasing token offsets, or NULL for a
+                                   dense batch.  Offsets are clamped into [0, seq_len];
+                                   decreasing offsets give unspecified (memory-safe)
+                                   results. */
+    const float* initial_state; /* device [batch, H, d_v, d_k], or NULL for zeros */
+    float* final_state;         /* device [batch, H, d_v, d_k], or NULL */
+    void* o;                    /* device [tokens, H, d_v], dtype */
+    void* workspace;            /* device scratch, 256-byte aligned */
+    size_t workspace_bytes;
+} rhz_gdr_prefill_args;
+
+/* One decode position for every (b, h), state updated in place.
+ * Replaces gated_delta_step (delta.rs:94-127), batched. */
+typedef struct rhz_gdr_decode_args {
+    int32_t batch;     /* B >= 1 */
+    int32_t heads;     /* H >= 1 */
+    int32_t d_k;       /* 1..256 */
+    int32_t d_v;       /* 1..1024 */
+    int32_t dtype;     /* rhz_dtype of q, k, v and o */
+    int32_t gate_kind; /* rhz_gate */
+    const void* q;     /* [B, H, d_k] */
+    const void* k;     /* [B, H, d_k] */
+    const void* v;     /* [B, H, d_v] */
+    const float* gate; /* [B, H] */
+    const float* beta; /* [B, H] */
+    float* state;      /* [B, H, d_v, d_k] fp32, read and written in place */
+    void* o;           /* [B, H, d_v] */
+} rhz_gdr_decode_args;
+
+/* Library identity. */
+int32_t rhz_gdr_abi_version(void);
+
+/* Human-readable name of a status code (static storage). */
+const char* rhz_status_string(int32_t status);
+
+/* Detail of the last non-OK status returned on the calling thread
+ * (thread-local storage, valid until the next call on that thread). */
+const char* rhz_last_error(void);
+
+/* Plan-time capability check (R4, SPEC.md:28-30): RHZ_OK when (op, dtype,
+ * d_k, d_v, algo) is supported, RHZ_ERR_UNSUPPORTED otherwise, and
+ * RHZ_ERR_INVALID_ARG for out-of-range enums or dimensions. */
+rhz_status rhz_gdr_query_support(int32_t op, int32_t dtype, int32_t d_k, int32_t d_v,
+                                 int32_t algo);
+
+/* Bytes of device workspace rhz_gdr_prefill needs for these arguments
+ * (pointers are not read).  0 when none is needed. */
+rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size_t* bytes);
+
+/* Gated delta-rule prefill (see rhz_gdr_prefill_args). */
+rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream);
+
+/* Gated delta-rule decode step (see rhz_gdr_decode_args). */
+rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* args, void* stream);
+
+/* Seeded synthetic inputs on the device, from the reference's Philox-4x32-10
+ * (crates/ops/src/rng.rs:43-90; elementwise.rs:5-12, 36-42, 125-128).
+ * Element e of the output takes normal #e of stream (seed, stream_id): the
+ * Box-Muller pair of Philox block e, computed in f64.  Per kind:
+ *   RHZ_FILL_NORMAL            mean + std * z
+ *   RHZ_FILL_UNIT_ROWS         z, L2-normalised over every run of row_len values
+ *                              (mean and std_dev unused; count % row_len == 0)
+ *   RHZ_FILL_SIGMOID           sigmoid(mean + std * z)
+ *   RHZ_FILL_NEG_SOFTPLUS      -softplus(mean + std * z)
+ * then rounded (f64 -> f32 -> bf16, round to nearest even) to out_dtype
+ * (RHZ_F64, RHZ_F32 or RHZ_BF16). */
+typedef enum rhz_fill_kind {
+    RHZ_FILL_NORMAL = 0,
+    RHZ_FILL_UNIT_ROWS = 1,
+    RHZ_FILL_SIGMOID = 2,
+    RHZ_FILL_NEG_SOFTPLUS = 3
+} rhz_fill_kind;
+
+rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count,
+                           int32_t row_len, double mean, double std_dev, int32_t out_dtype,
+                           void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RHIZOME_GDR_H */

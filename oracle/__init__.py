@@ -1,0 +1,5 @@
+"""CPU f64 oracle of the gated delta-rule forward -- test infrastructure only.
+
+Imported by tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg; never by the product package.
+"""

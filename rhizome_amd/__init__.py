@@ -1,0 +1,10 @@
+"""rhizome_amd -- MI355X (gfx950) gated delta-rule forward behind a C ABI.
+
+The compute lives in librhizome_gdr.so (hand-written HIP kernels, built by
+``python -m rhizome_amd.build``); this package is its torch-tensor front
+end.  Importing the package does not load the library; the first call does,
+and raises if the library is missing.
+"""
+from .gdr import decode_step, philox_fill, prefill, query_support  # noqa: F401
+
+__all__ = ["prefill", "decode_step", "philox_fill", "query_support"]

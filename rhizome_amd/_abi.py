@@ -1,0 +1,110 @@
+"""ctypes mirror of include/rhizome_gdr.h and the loader of librhizome_gdr.so.
+
+The library is loaded from this package directory only (built in-tree by
+rhizome_amd.build); if it is missing, loading raises -- there is no
+fallback implementation of any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from ctypes import POINTER, Structure, c_char_p, c_double, c_int32, c_int64, c_size_t, c_uint64, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "librhizome_gdr.so")
+HEADER = os.path.join(ROOT, "include", "rhizome_gdr.h")
+
+# rhz_status
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, 1, 2, 3, 4
+# rhz_dtype
+F32, BF16, F64 = 0, 1, 2
+# rhz_gate
+GATE_LOG_ALPHA, GATE_ALPHA = 0, 1
+# rhz_algo
+ALGO_AUTO, ALGO_RECURRENT, ALGO_CHUNKED = 0, 1, 2
+# rhz_op
+OP_DELTA_SCAN, OP_DELTA_STEP = 0, 1
+# rhz_fill_kind
+FILL_NORMAL, FILL_UNIT_ROWS, FILL_SIGMOID, FILL_NEG_SOFTPLUS = 0, 1, 2, 3
+
+
+class PrefillArgs(Structure):
+    _fields_ = [
+        ("batch", c_int32), ("seq_len", c_int32), ("heads", c_int32), ("d_k", c_int32),
+        ("d_v", c_int32), ("chunk", c_int32), ("dtype", c_int32), ("gate_kind", c_int32),
+        ("algo", c_int32),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("gate", c_void_p), ("beta", c_void_p),
+        ("cu_seqlens", c_void_p), ("initial_state", c_void_p), ("final_state", c_void_p),
+        ("o", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class DecodeArgs(Structure):
+    _fields_ = [
+        ("batch", c_int32), ("heads", c_int32), ("d_k", c_int32), ("d_v", c_int32),
+        ("dtype", c_int32), ("gate_kind", c_int32),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("gate", c_void_p), ("beta", c_void_p),
+        ("state", c_void_p), ("o", c_void_p),
+    ]
+
+
+class GdrError(RuntimeError):
+    """A non-OK rhz_status, with the library's detail message."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        super().__init__(f"{status_string(status)}: {message}")
+
+
+_lib = None
+
+
+def declared_functions() -> list[str]:
+    """Names of the functions declared in include/rhizome_gdr.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rhz_\w+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m rhizome_amd.build` "
+                "(the gated delta-rule ops have no non-HIP implementation)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.rhz_gdr_abi_version.restype = c_int32
+        L.rhz_status_string.argtypes = [c_int32]
+        L.rhz_status_string.restype = c_char_p
+        L.rhz_last_error.restype = c_char_p
+        L.rhz_gdr_query_support.argtypes = [c_int32] * 5
+        L.rhz_gdr_query_support.restype = c_int32
+        L.rhz_gdr_prefill_workspace_size.argtypes = [POINTER(PrefillArgs), POINTER(c_size_t)]
+        L.rhz_gdr_prefill_workspace_size.restype = c_int32
+        L.rhz_gdr_prefill.argtypes = [POINTER(PrefillArgs), c_void_p]
+        L.rhz_gdr_prefill.restype = c_int32
+        L.rhz_gdr_decode_step.argtypes = [POINTER(DecodeArgs), c_void_p]
+        L.rhz_gdr_decode_step.restype = c_int32
+        L.rhz_philox_fill.argtypes = [c_int32, c_uint64, c_uint64, c_int64, c_int32, c_double,
+                                      c_double, c_int32, c_void_p, c_void_p]
+        L.rhz_philox_fill.restype = c_int32
+        if L.rhz_gdr_abi_version() != 1:
+            raise RuntimeError("librhizome_gdr.so ABI version mismatch")
+        _lib = L
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().rhz_status_string(status).decode()
+
+
+def last_error() -> str:
+    return lib().rhz_last_error().decode()
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise GdrError(status, last_error())

@@ -1,0 +1,224 @@
+// gdr_abi.cpp -- the extern "C" boundary of librhizome_gdr.so: argument
+// validation (complete before any HIP call, so every error path can be
+// exercised without a GPU), algorithm selection, workspace sizing and
+// dispatch to the kernel launchers.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gdr_internal.hpp"
+#include "rhizome_gdr.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+rhz_status fail(rhz_status s, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return s;
+}
+
+rhz_status ok() {
+    g_last_error.clear();
+    return RHZ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kMaxIndex = INT32_MAX;
+
+// Validates a prefill call and resolves its algorithm.  Pointers are checked
+// only when check_ptrs is set (the workspace query reads none).
+rhz_status check_prefill(const rhz_gdr_prefill_args* a, bool check_ptrs, int* algo_out) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->batch < 1) return fail(RHZ_ERR_INVALID_ARG, "batch must be >= 1 (got %d)", a->batch);
+    if (a->seq_len < 0) return fail(RHZ_ERR_INVALID_ARG, "seq_len must be >= 0 (got %d)", a->seq_len);
+    if (a->heads < 1) return fail(RHZ_ERR_INVALID_ARG, "heads must be >= 1 (got %d)", a->heads);
+    if (a->d_k < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k must be >= 1 (got %d)", a->d_k);
+    if (a->d_v < 1) return fail(RHZ_ERR_INVALID_ARG, "d_v must be >= 1 (got %d)", a->d_v);
+    if (a->chunk < 1) return fail(RHZ_ERR_INVALID_ARG, "chunk must be >= 1 (got %d)", a->chunk);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (a->gate_kind != RHZ_GATE_LOG_ALPHA && a->gate_kind != RHZ_GATE_ALPHA)
+        return fail(RHZ_ERR_INVALID_ARG, "gate_kind must be RHZ_GATE_LOG_ALPHA or RHZ_GATE_ALPHA (got %d)",
+                    a->gate_kind);
+    if (a->algo < RHZ_ALGO_AUTO || a->algo > RHZ_ALGO_CHUNKED)
+        return fail(RHZ_ERR_INVALID_ARG, "algo must be AUTO, RECURRENT or CHUNKED (got %d)", a->algo);
+    if (a->d_k > 256) return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d exceeds the supported 256", a->d_k);
+    if (a->d_v > 1024) return fail(RHZ_ERR_UNSUPPORTED, "d_v = %d exceeds the supported 1024", a->d_v);
+    const int64_t tokens = a->cu_seqlens ? (int64_t)a->seq_len : (int64_t)a->batch * a->seq_len;
+    if (tokens * a->heads > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "tokens * heads = %lld exceeds 2^31 - 1", (long long)(tokens * a->heads));
+    const int64_t units = (int64_t)a->batch * a->heads;
+    if (units * ((a->d_v + 7) / 8) > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "batch * heads = %lld is too large", (long long)units);
+
+    int algo = a->algo;
+    const bool chunk_dims = rhz::chunked_supported(a->d_k, a->d_v);
+    if (algo == RHZ_ALGO_AUTO) algo = (a->dtype == RHZ_BF16 && chunk_dims) ? RHZ_ALGO_CHUNKED : RHZ_ALGO_RECURRENT;
+    if (algo == RHZ_ALGO_CHUNKED) {
+        if (a->dtype != RHZ_BF16) return fail(RHZ_ERR_UNSUPPORTED, "CHUNKED needs bf16 q/k/v (dtype %d)", a->dtype);
+        if (!chunk_dims)
+            return fail(RHZ_ERR_UNSUPPORTED,
+                        "CHUNKED needs d_k in 8..128 and d_v >= 8, both multiples of 8 (got d_k=%d d_v=%d)",
+                        a->d_k, a->d_v);
+    }
+    *algo_out = algo;
+    if (!check_ptrs) return ok();
+
+    if (tokens > 0) {
+        if (!a->q) return fail(RHZ_ERR_INVALID_ARG, "q is NULL");
+        if (!a->k) return fail(RHZ_ERR_INVALID_ARG, "k is NULL");
+        if (!a->v) return fail(RHZ_ERR_INVALID_ARG, "v is NULL");
+        if (!a->gate) return fail(RHZ_ERR_INVALID_ARG, "gate is NULL");
+        if (!a->beta) return fail(RHZ_ERR_INVALID_ARG, "beta is NULL");
+        if (!a->o) return fail(RHZ_ERR_INVALID_ARG, "o is NULL");
+    }
+    if (algo == RHZ_ALGO_CHUNKED) {
+        const void* ptrs[] = {a->q, a->k, a->v, a->o, a->initial_state, a->final_state};
+        const char* names[] = {"q", "k", "v", "o", "initial_state", "final_state"};
+        for (int i = 0; i < 6; ++i)
+            if (!aligned16(ptrs[i]))
+                return fail(RHZ_ERR_INVALID_ARG, "CHUNKED needs %s 16-byte aligned", names[i]);
+    } else {
+        const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+        const void* ptrs[] = {a->q, a->k, a->v, a->o};
+        const char* names[] = {"q", "k", "v", "o"};
+        for (int i = 0; i < 4; ++i)
+            if (reinterpret_cast<uintptr_t>(ptrs[i]) % ea)
+                return fail(RHZ_ERR_INVALID_ARG, "%s is not aligned to its element size", names[i]);
+    }
+    if (reinterpret_cast<uintptr_t>(a->gate) % 4 || reinterpret_cast<uintptr_t>(a->beta) % 4 ||
+        reinterpret_cast<uintptr_t>(a->initial_state) % 4 || reinterpret_cast<uintptr_t>(a->final_state) % 4 ||
+        reinterpret_cast<uintptr_t>(a->cu_seqlens) % 4)
+        return fail(RHZ_ERR_INVALID_ARG, "fp32/int32 tensors must be 4-byte aligned");
+    return ok();
+}
+
+rhz_status hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return ok();
+    return fail(RHZ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t rhz_gdr_abi_version(void) { return RHZ_GDR_ABI_VERSION; }
+
+const char* rhz_status_string(int32_t status) {
+    switch (status) {
+        case RHZ_OK: return "RHZ_OK";
+        case RHZ_ERR_INVALID_ARG: return "RHZ_ERR_INVALID_ARG";
+        case RHZ_ERR_UNSUPPORTED: return "RHZ_ERR_UNSUPPORTED";
+        case RHZ_ERR_WORKSPACE: return "RHZ_ERR_WORKSPACE";
+        case RHZ_ERR_HIP: return "RHZ_ERR_HIP";
+        default: return "RHZ_ERR_UNKNOWN";
+    }
+}
+
+const char* rhz_last_error(void) { return g_last_error.c_str(); }
+
+rhz_status rhz_gdr_query_support(int32_t op, int32_t dtype, int32_t d_k, int32_t d_v, int32_t algo) {
+    if (op != RHZ_OP_DELTA_SCAN && op != RHZ_OP_DELTA_STEP) return fail(RHZ_ERR_INVALID_ARG, "unknown op %d", op);
+    if (dtype != RHZ_F32 && dtype != RHZ_BF16) return fail(RHZ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (algo < RHZ_ALGO_AUTO || algo > RHZ_ALGO_CHUNKED) return fail(RHZ_ERR_INVALID_ARG, "unknown algo %d", algo);
+    if (d_k < 1 || d_v < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k and d_v must be >= 1");
+    if (d_k > 256 || d_v > 1024)
+        return fail(RHZ_ERR_UNSUPPORTED, "d_k <= 256 and d_v <= 1024 are supported (got %d, %d)", d_k, d_v);
+    if (op == RHZ_OP_DELTA_STEP) {
+        if (algo == RHZ_ALGO_CHUNKED) return fail(RHZ_ERR_UNSUPPORTED, "the decode step has no CHUNKED algorithm");
+        return ok();
+    }
+    if (algo == RHZ_ALGO_CHUNKED) {
+        if (dtype != RHZ_BF16) return fail(RHZ_ERR_UNSUPPORTED, "CHUNKED needs bf16 inputs");
+        if (!rhz::chunked_supported(d_k, d_v))
+            return fail(RHZ_ERR_UNSUPPORTED, "CHUNKED needs d_k in 8..128 and d_v >= 8, multiples of 8");
+    }
+    return ok();
+}
+
+rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size_t* bytes) {
+    if (!bytes) return fail(RHZ_ERR_INVALID_ARG, "bytes is NULL");
+    int algo = 0;
+    const rhz_status s = check_prefill(args, false, &algo);
+    if (s != RHZ_OK) return s;
+    *bytes = algo == RHZ_ALGO_CHUNKED ? rhz::chunked_workspace_bytes(*args) : 0;
+    return ok();
+}
+
+rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) {
+    int algo = 0;
+    const rhz_status s = check_prefill(args, true, &algo);
+    if (s != RHZ_OK) return s;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (algo == RHZ_ALGO_CHUNKED) {
+        const size_t need = rhz::chunked_workspace_bytes(*args);
+        if (!args->workspace) return fail(RHZ_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", need);
+        if (args->workspace_bytes < need)
+            return fail(RHZ_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", args->workspace_bytes, need);
+        if (reinterpret_cast<uintptr_t>(args->workspace) & 255u)
+            return fail(RHZ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+        return hip_status(rhz::launch_chunked(*args, st), "chunked prefill launch");
+    }
+    return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");
+}
+
+rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->batch < 1) return fail(RHZ_ERR_INVALID_ARG, "batch must be >= 1 (got %d)", a->batch);
+    if (a->heads < 1) return fail(RHZ_ERR_INVALID_ARG, "heads must be >= 1 (got %d)", a->heads);
+    if (a->d_k < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k must be >= 1 (got %d)", a->d_k);
+    if (a->d_v < 1) return fail(RHZ_ERR_INVALID_ARG, "d_v must be >= 1 (got %d)", a->d_v);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (a->gate_kind != RHZ_GATE_LOG_ALPHA && a->gate_kind != RHZ_GATE_ALPHA)
+        return fail(RHZ_ERR_INVALID_ARG, "gate_kind must be RHZ_GATE_LOG_ALPHA or RHZ_GATE_ALPHA (got %d)",
+                    a->gate_kind);
+    if (a->d_k > 256) return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d exceeds the supported 256", a->d_k);
+    if (a->d_v > 1024) return fail(RHZ_ERR_UNSUPPORTED, "d_v = %d exceeds the supported 1024", a->d_v);
+    if ((int64_t)a->batch * a->heads > kMaxIndex) return fail(RHZ_ERR_INVALID_ARG, "batch * heads exceeds 2^31 - 1");
+    if (!a->q) return fail(RHZ_ERR_INVALID_ARG, "q is NULL");
+    if (!a->k) return fail(RHZ_ERR_INVALID_ARG, "k is NULL");
+    if (!a->v) return fail(RHZ_ERR_INVALID_ARG, "v is NULL");
+    if (!a->gate) return fail(RHZ_ERR_INVALID_ARG, "gate is NULL");
+    if (!a->beta) return fail(RHZ_ERR_INVALID_ARG, "beta is NULL");
+    if (!a->state) return fail(RHZ_ERR_INVALID_ARG, "state is NULL");
+    if (!a->o) return fail(RHZ_ERR_INVALID_ARG, "o is NULL");
+    const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+    const void* ptrs[] = {a->q, a->k, a->v, a->o};
+    const char* names[] = {"q", "k", "v", "o"};
+    for (int i = 0; i < 4; ++i)
+        if (reinterpret_cast<uintptr_t>(ptrs[i]) % ea)
+            return fail(RHZ_ERR_INVALID_ARG, "%s is not aligned to its element size", names[i]);
+    if (reinterpret_cast<uintptr_t>(a->gate) % 4 || reinterpret_cast<uintptr_t>(a->beta) % 4 ||
+        reinterpret_cast<uintptr_t>(a->state) % 4)
+        return fail(RHZ_ERR_INVALID_ARG, "fp32 tensors must be 4-byte aligned");
+    return hip_status(rhz::launch_decode(*a, static_cast<hipStream_t>(stream)), "decode step launch");
+}
+
+rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count, int32_t row_len,
+                           double mean, double std_dev, int32_t out_dtype, void* out, void* stream) {
+    if (kind < RHZ_FILL_NORMAL || kind > RHZ_FILL_NEG_SOFTPLUS) return fail(RHZ_ERR_INVALID_ARG, "unknown kind %d", kind);
+    if (count < 0) return fail(RHZ_ERR_INVALID_ARG, "count must be >= 0");
+    if (out_dtype != RHZ_F32 && out_dtype != RHZ_BF16 && out_dtype != RHZ_F64)
+        return fail(RHZ_ERR_INVALID_ARG, "out_dtype must be RHZ_F64, RHZ_F32 or RHZ_BF16");
+    if (kind == RHZ_FILL_UNIT_ROWS && (row_len < 1 || count % row_len != 0))
+        return fail(RHZ_ERR_INVALID_ARG, "UNIT_ROWS needs row_len >= 1 dividing count");
+    if (count > 0 && !out) return fail(RHZ_ERR_INVALID_ARG, "out is NULL");
+    if (count > ((int64_t)1 << 40)) return fail(RHZ_ERR_INVALID_ARG, "count too large");
+    return hip_status(rhz::launch_philox_fill(kind, seed, stream_id, count, row_len, mean, std_dev, out_dtype, out,
+                                              static_cast<hipStream_t>(stream)),
+                      "philox fill launch");
+}
+
+}  // extern "C"

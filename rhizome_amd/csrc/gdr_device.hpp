@@ -1,0 +1,102 @@
+// gdr_device.hpp -- device helpers shared by the gfx950 gated delta-rule kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rhz {
+
+// Vector types of the gfx950 MFMA builtins.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Chunk length of the WY/UT prefill and the log-decay floor: a per-token
+// log-decay below kLogDecayFloor (alpha < 1.8e-35, including alpha = 0) is
+// raised to it, so every exponent stays finite; the state it carries over is
+// scaled by at most 1.8e-35.
+constexpr int kChunk = 64;
+constexpr float kLogDecayFloor = -80.0f;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// float -> bf16, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+// float -> fp16 bits, round to nearest even.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    return uint32_t(f32_to_f16(lo)) | (uint32_t(f32_to_f16(hi)) << 16);
+}
+
+// 2^e as a float, e clamped to the normal range [-126, 127].
+__device__ __forceinline__ float exp2i(int e) {
+    e = min(max(e, -126), 127);
+    return __int_as_float((e + 127) << 23);
+}
+
+// floor(log2(m)) for a positive normal float m (-127 for zero/subnormal).
+__device__ __forceinline__ int ilog2f(float m) { return int((__float_as_uint(m) >> 23) & 0xffu) - 127; }
+
+// Maximum over the 64 lanes of a wave (every lane receives it).
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
+    return x;
+}
+
+// Element loads of the two input dtypes, widened to float.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static __device__ __forceinline__ float load(const float* p, long i) { return p[i]; }
+    static __device__ __forceinline__ void store(float* p, long i, float x) { p[i] = x; }
+};
+template <> struct Elem<uint16_t> {
+    static __device__ __forceinline__ float load(const uint16_t* p, long i) { return bf16_to_f32(p[i]); }
+    static __device__ __forceinline__ void store(uint16_t* p, long i, float x) { p[i] = f32_to_bf16(x); }
+};
+
+// Four consecutive elements widened to float (caller guarantees alignment:
+// 16 bytes for float, 8 bytes for bf16).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t* p) {
+    uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64);
+// every lane of the group receives the group's sum.  Fixed butterfly order,
+// so the result is deterministic.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+// Gate value -> log-decay g (<= 0 expected), floored at kLogDecayFloor.
+__device__ __forceinline__ float log_decay(float gate, int gate_is_alpha) {
+    float g = gate_is_alpha ? logf(gate) : gate;
+    return fmaxf(g, kLogDecayFloor);  // also maps -inf (alpha = 0) and NaN-free logs
+}
+
+// Gate value -> alpha.
+__device__ __forceinline__ float decay_factor(float gate, int gate_is_alpha) {
+    return gate_is_alpha ? gate : expf(gate);
+}
+
+}  // namespace rhz

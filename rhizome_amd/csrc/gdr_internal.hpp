@@ -1,0 +1,31 @@
+// gdr_internal.hpp -- host-side launch interface between the C ABI layer
+// (gdr_abi.cpp) and the kernel files.  Arguments are validated by the
+// caller before any of these run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rhizome_gdr.h"
+
+namespace rhz {
+
+// Token-sequential fp32 recurrence over a dense or packed batch.
+hipError_t launch_recurrent(const rhz_gdr_prefill_args& a, hipStream_t stream);
+
+// One decode position for every (b, h), state in place.
+hipError_t launch_decode(const rhz_gdr_decode_args& a, hipStream_t stream);
+
+// Chunked WY/UT prefill (bf16 in, fp32 state).  Requires d_k % 8 == 0,
+// d_k <= 128, d_v % 8 == 0 and 16-byte aligned tensors.
+bool chunked_supported(int d_k, int d_v);
+size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a);
+hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream);
+
+// Device Philox-4x32-10 fill.
+hipError_t launch_philox_fill(int kind, uint64_t seed, uint64_t stream_id, int64_t count,
+                              int row_len, double mean, double std_dev, int out_dtype, void* out,
+                              hipStream_t stream);
+
+}  // namespace rhz

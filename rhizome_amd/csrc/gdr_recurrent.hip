@@ -1,0 +1,297 @@
+// gdr_recurrent.hip -- row-parallel fp32 gated delta-rule kernels for gfx950:
+//
+//   gdr_decode_kernel     one position for every (b, h), state streamed from
+//                         HBM and written back in place (gated_delta_step,
+//                         crates/ops/src/delta.rs:94-127, batched);
+//   gdr_recurrent_kernel  the same update carried token by token through a
+//                         whole sequence with the state rows in registers
+//                         (gated_delta_sequential, delta.rs:133-154, without
+//                         its t = 0 reset; the fp32-input prefill path).
+//
+// Rows of S are independent (row i only reads v_i and its own row), so
+// both kernels give each row to a group of LPR = d_k_max / 16 lanes; lane li
+// of a group holds columns c*4*LPR + 4*li + e (c, e in 0..3), so every
+// 16-byte load of a wave covers whole contiguous row segments.  Per row and
+// token the two dot products S_i.k and S_i.q and the shared k.q are summed
+// over the group with a fixed butterfly, then
+//     c_i  = beta * (v_i - alpha * (S_i.k))
+//     o_i  = alpha * (S_i.q) + c_i * (k.q)        (= S_i' . q)
+//     S_i' = alpha * S_i + c_i * k                (one FMA per element)
+// so the state is read once and written once per position.
+
+#include "gdr_device.hpp"
+#include "gdr_internal.hpp"
+
+namespace rhz {
+namespace {
+
+struct StepParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* gate;
+    const float* beta;
+    float* state;
+    void* o;
+    int d_k, d_v, gate_is_alpha;
+};
+
+struct SeqParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* gate;
+    const float* beta;
+    const int* cu_seqlens;
+    const float* init;
+    float* fin;
+    void* o;
+    int seq_len, heads, d_k, d_v, gate_is_alpha;
+};
+
+// The 16 columns of a row held by lane li of its group (zero outside [0, n)).
+template <int LPR, bool VEC, typename T>
+__device__ __forceinline__ void load_slice(const T* row, int li, int n, float (&x)[16]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int col = c * 4 * LPR + 4 * li;
+        if (VEC) {
+            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (col < n) f = load4(row + col);
+            x[4 * c + 0] = f.x;
+            x[4 * c + 1] = f.y;
+            x[4 * c + 2] = f.z;
+            x[4 * c + 3] = f.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * c + e] = (col + e < n) ? Elem<T>::load(row, col + e) : 0.f;
+        }
+    }
+}
+
+template <int LPR, bool VEC>
+__device__ __forceinline__ void store_slice(float* row, int li, int n, const float (&x)[16]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int col = c * 4 * LPR + 4 * li;
+        if (VEC) {
+            if (col < n)
+                *reinterpret_cast<float4*>(row + col) =
+                    make_float4(x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < n) row[col + e] = x[4 * c + e];
+        }
+    }
+}
+
+__device__ __forceinline__ float dot16(const float (&a)[16], const float (&b)[16]) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        s0 += a[4 * c + 0] * b[4 * c + 0];
+        s1 += a[4 * c + 1] * b[4 * c + 1];
+        s2 += a[4 * c + 2] * b[4 * c + 2];
+        s3 += a[4 * c + 3] * b[4 * c + 3];
+    }
+    return (s0 + s1) + (s2 + s3);
+}
+
+// Sequence bounds of packed sequence `seq`, clamped into [0, total].
+__device__ __forceinline__ void seq_bounds(const int* cu, int seq, int seq_len, int& t0, int& t1) {
+    if (cu) {
+        t0 = min(max(cu[seq], 0), seq_len);
+        t1 = min(max(cu[seq + 1], t0), seq_len);
+    } else {
+        t0 = seq * seq_len;
+        t1 = t0 + seq_len;
+    }
+}
+
+// ---------------------------------------------------------------- decode
+// Grid: x = b*H + h, y = block of P*RPP rows.  256 threads, RPP = 256/LPR
+// rows per pass; all of a lane's state loads are issued before any use.
+template <int LPR, int P, bool VEC, typename T>
+__global__ __launch_bounds__(256) void gdr_decode_kernel(StepParams p) {
+    constexpr int RPP = 256 / LPR;
+    const int bh = blockIdx.x;
+    const int li = threadIdx.x % LPR;
+    const int rl = threadIdx.x / LPR;
+    const int dk = p.d_k, dv = p.d_v;
+    const T* q = static_cast<const T*>(p.q) + (long)bh * dk;
+    const T* k = static_cast<const T*>(p.k) + (long)bh * dk;
+    const T* v = static_cast<const T*>(p.v) + (long)bh * dv;
+    T* o = static_cast<T*>(p.o) + (long)bh * dv;
+    float* S = p.state + (long)bh * dv * dk;
+    const int rbase = blockIdx.y * (P * RPP) + rl;
+
+    float s[P][16];
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+        const int r = rbase + pp * RPP;
+        if (r < dv) {
+            load_slice<LPR, VEC, float>(S + (long)r * dk, li, dk, s[pp]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[pp][e] = 0.f;
+        }
+    }
+    float kr[16], qr[16];
+    load_slice<LPR, VEC, T>(k, li, dk, kr);
+    load_slice<LPR, VEC, T>(q, li, dk, qr);
+    const float alpha = decay_factor(p.gate[bh], p.gate_is_alpha);
+    const float beta = p.beta[bh];
+    const float kq = group_sum<LPR>(dot16(kr, qr));
+
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+        const int r = rbase + pp * RPP;
+        const float sk = group_sum<LPR>(dot16(s[pp], kr));
+        const float sq = group_sum<LPR>(dot16(s[pp], qr));
+        if (r < dv) {
+            const float vi = Elem<T>::load(v, r);
+            const float c = beta * (vi - alpha * sk);
+            const float oi = alpha * sq + c * kq;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
+            store_slice<LPR, VEC>(S + (long)r * dk, li, dk, s[pp]);
+            if (li == 0) Elem<T>::store(o, r, oi);
+        }
+    }
+}
+
+// ------------------------------------------------------- recurrent prefill
+// Grid: x = seq*H + h, y = block of RPW = 64/LPR rows; one wave per block.
+// The next token's k, q, v and gates are loaded while the current one is
+// applied.
+template <int LPR, bool VEC, typename T>
+__global__ __launch_bounds__(64) void gdr_recurrent_kernel(SeqParams p) {
+    constexpr int RPW = 64 / LPR;
+    const int unit = blockIdx.x;
+    const int seq = unit / p.heads, h = unit % p.heads;
+    const int li = threadIdx.x % LPR;
+    const int r = blockIdx.y * RPW + threadIdx.x / LPR;
+    const int dk = p.d_k, dv = p.d_v, H = p.heads;
+    const bool row_ok = r < dv;
+    int t0, t1;
+    seq_bounds(p.cu_seqlens, seq, p.seq_len, t0, t1);
+
+    float s[16];
+    if (p.init && row_ok) {
+        load_slice<LPR, VEC, float>(p.init + ((long)unit * dv + r) * dk, li, dk, s);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = 0.f;
+    }
+    const T* qp = static_cast<const T*>(p.q);
+    const T* kp = static_cast<const T*>(p.k);
+    const T* vp = static_cast<const T*>(p.v);
+    T* op = static_cast<T*>(p.o);
+
+    float kn[16], qn[16], vn = 0.f, gn = 0.f, bn = 0.f;
+    auto fetch = [&](int t) {
+        const long th = (long)t * H + h;
+        load_slice<LPR, VEC, T>(kp + th * dk, li, dk, kn);
+        load_slice<LPR, VEC, T>(qp + th * dk, li, dk, qn);
+        vn = row_ok ? Elem<T>::load(vp, th * dv + r) : 0.f;
+        gn = p.gate[th];
+        bn = p.beta[th];
+    };
+    if (t0 < t1) fetch(t0);
+    for (int t = t0; t < t1; ++t) {
+        float kr[16], qr[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            kr[e] = kn[e];
+            qr[e] = qn[e];
+        }
+        const float vi = vn, ga = gn, be = bn;
+        if (t + 1 < t1) fetch(t + 1);
+        const float alpha = decay_factor(ga, p.gate_is_alpha);
+        const float kq = group_sum<LPR>(dot16(kr, qr));
+        const float sk = group_sum<LPR>(dot16(s, kr));
+        const float sq = group_sum<LPR>(dot16(s, qr));
+        const float c = be * (vi - alpha * sk);
+        const float oi = alpha * sq + c * kq;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = alpha * s[e] + c * kr[e];
+        if (li == 0 && row_ok) Elem<T>::store(op, ((long)t * H + h) * dv + r, oi);
+    }
+    if (p.fin && row_ok) store_slice<LPR, VEC>(p.fin + ((long)unit * dv + r) * dk, li, dk, s);
+}
+
+int lanes_per_row(int d_k) { return d_k <= 32 ? 2 : d_k <= 64 ? 4 : d_k <= 128 ? 8 : 16; }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+template <int LPR, int P, bool VEC, typename T>
+hipError_t decode_go(const StepParams& sp, int units, int dv, hipStream_t st) {
+    constexpr int RPP = 256 / LPR;
+    dim3 grid(units, (dv + P * RPP - 1) / (P * RPP));
+    hipLaunchKernelGGL((gdr_decode_kernel<LPR, P, VEC, T>), grid, dim3(256), 0, st, sp);
+    return hipGetLastError();
+}
+
+template <int LPR, bool VEC, typename T>
+hipError_t decode_pick_p(const StepParams& sp, int units, int dv, hipStream_t st) {
+    constexpr int RPP = 256 / LPR;
+    const int passes = (dv + RPP - 1) / RPP;
+    if (passes >= 4) return decode_go<LPR, 4, VEC, T>(sp, units, dv, st);
+    if (passes == 3 || passes == 2) return decode_go<LPR, 2, VEC, T>(sp, units, dv, st);
+    return decode_go<LPR, 1, VEC, T>(sp, units, dv, st);
+}
+
+template <bool VEC, typename T>
+hipError_t decode_pick_lpr(const StepParams& sp, int units, int dk, int dv, hipStream_t st) {
+    switch (lanes_per_row(dk)) {
+        case 2: return decode_pick_p<2, VEC, T>(sp, units, dv, st);
+        case 4: return decode_pick_p<4, VEC, T>(sp, units, dv, st);
+        case 8: return decode_pick_p<8, VEC, T>(sp, units, dv, st);
+        default: return decode_pick_p<16, VEC, T>(sp, units, dv, st);
+    }
+}
+
+template <bool VEC, typename T>
+hipError_t recurrent_pick_lpr(const SeqParams& sp, int units, int dk, int dv, hipStream_t st) {
+    const int lpr = lanes_per_row(dk);
+    const int rpw = 64 / lpr;
+    dim3 grid(units, (dv + rpw - 1) / rpw);
+    switch (lpr) {
+        case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<2, VEC, T>), grid, dim3(64), 0, st, sp); break;
+        case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<4, VEC, T>), grid, dim3(64), 0, st, sp); break;
+        case 8: hipLaunchKernelGGL((gdr_recurrent_kernel<8, VEC, T>), grid, dim3(64), 0, st, sp); break;
+        default: hipLaunchKernelGGL((gdr_recurrent_kernel<16, VEC, T>), grid, dim3(64), 0, st, sp); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(const rhz_gdr_decode_args& a, hipStream_t st) {
+    StepParams sp{a.q, a.k, a.v, a.gate, a.beta, a.state, a.o, a.d_k, a.d_v, a.gate_kind == RHZ_GATE_ALPHA};
+    const int units = a.batch * a.heads;
+    const size_t ea = a.dtype == RHZ_F32 ? 16 : 8;
+    const bool vec = (a.d_k % 4 == 0) && aligned(a.q, ea) && aligned(a.k, ea) && aligned(a.state, 16);
+    if (a.dtype == RHZ_F32)
+        return vec ? decode_pick_lpr<true, float>(sp, units, a.d_k, a.d_v, st)
+                   : decode_pick_lpr<false, float>(sp, units, a.d_k, a.d_v, st);
+    return vec ? decode_pick_lpr<true, uint16_t>(sp, units, a.d_k, a.d_v, st)
+               : decode_pick_lpr<false, uint16_t>(sp, units, a.d_k, a.d_v, st);
+}
+
+hipError_t launch_recurrent(const rhz_gdr_prefill_args& a, hipStream_t st) {
+    SeqParams sp{a.q, a.k, a.v, a.gate, a.beta, a.cu_seqlens, a.initial_state, a.final_state, a.o,
+                 a.seq_len, a.heads, a.d_k, a.d_v, a.gate_kind == RHZ_GATE_ALPHA};
+    const int units = a.batch * a.heads;
+    const size_t ea = a.dtype == RHZ_F32 ? 16 : 8;
+    const bool vec = (a.d_k % 4 == 0) && aligned(a.q, ea) && aligned(a.k, ea) &&
+                     aligned(a.initial_state, 16) && aligned(a.final_state, 16);
+    if (a.dtype == RHZ_F32)
+        return vec ? recurrent_pick_lpr<true, float>(sp, units, a.d_k, a.d_v, st)
+                   : recurrent_pick_lpr<false, float>(sp, units, a.d_k, a.d_v, st);
+    return vec ? recurrent_pick_lpr<true, uint16_t>(sp, units, a.d_k, a.d_v, st)
+               : recurrent_pick_lpr<false, uint16_t>(sp, units, a.d_k, a.d_v, st);
+}
+
+}  // namespace rhz

@@ -1,0 +1,170 @@
+"""Torch-tensor front end of the gated delta-rule C ABI (librhizome_gdr.so).
+
+PyTorch is used only for device memory and streams: every function checks
+shapes, fills the C argument struct with raw device pointers and calls the
+library on the current HIP stream.  Nothing here computes the op.
+
+Layouts follow include/rhizome_gdr.h: q, k [B, T, H, d_k] (dense) or
+[tokens, H, d_k] with ``cu_seqlens``; v, o likewise with d_v; gates and
+beta [B, T, H] / [tokens, H] fp32; states [N, H, d_v, d_k] fp32 with
+S[i][j] = state[..., i, j] (i = value row, j = key column, the layout of
+crates/ops/src/delta.rs:63).
+"""
+from __future__ import annotations
+
+from ctypes import byref, c_size_t
+
+import torch
+
+from . import _abi
+from ._abi import GdrError  # noqa: F401  (re-exported)
+
+_ALGOS = {"auto": _abi.ALGO_AUTO, "recurrent": _abi.ALGO_RECURRENT, "chunked": _abi.ALGO_CHUNKED}
+_DTYPES = {torch.float32: _abi.F32, torch.bfloat16: _abi.BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("all tensors must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("all tensors must be contiguous")
+    return t.data_ptr() or None
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def _gate(g, alpha):
+    if (g is None) == (alpha is None):
+        raise ValueError("pass exactly one of g (log-decay) and alpha")
+    return (g, _abi.GATE_LOG_ALPHA) if g is not None else (alpha, _abi.GATE_ALPHA)
+
+
+def prefill_args(q, k, v, gate, beta, gate_kind, cu_seqlens=None, initial_state=None,
+                 final_state=None, o=None, algo="auto", chunk=64, workspace=None) -> _abi.PrefillArgs:
+    """Fill the C argument struct (shapes are read from the tensors)."""
+    if cu_seqlens is None:
+        B, T, H, dk = q.shape
+        batch, seq_len = B, T
+    else:
+        _, H, dk = q.shape
+        batch, seq_len = cu_seqlens.numel() - 1, q.shape[0]
+    dv = v.shape[-1]
+    a = _abi.PrefillArgs()
+    a.batch, a.seq_len, a.heads, a.d_k, a.d_v = batch, seq_len, H, dk, dv
+    a.chunk = chunk
+    a.dtype = _DTYPES[q.dtype]
+    a.gate_kind = gate_kind
+    a.algo = _ALGOS[algo]
+    a.q, a.k, a.v, a.gate, a.beta = _ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta)
+    a.cu_seqlens = _ptr(cu_seqlens)
+    a.initial_state, a.final_state, a.o = _ptr(initial_state), _ptr(final_state), _ptr(o)
+    if workspace is not None:
+        a.workspace, a.workspace_bytes = _ptr(workspace), workspace.numel()
+    return a
+
+
+def workspace_bytes(args: _abi.PrefillArgs) -> int:
+    n = c_size_t(0)
+    _abi.check(_abi.lib().rhz_gdr_prefill_workspace_size(byref(args), byref(n)))
+    return n.value
+
+
+def _check_prefill_shapes(q, k, v, gate, beta, cu_seqlens, initial_state):
+    dense = cu_seqlens is None
+    nd = 4 if dense else 3
+    if q.dim() != nd or k.shape != q.shape or v.dim() != nd or v.shape[:-1] != q.shape[:-1]:
+        raise ValueError(f"q/k/v shapes {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)} "
+                         f"do not match the {'dense' if dense else 'packed'} layout")
+    if gate.shape != q.shape[:-1] or beta.shape != q.shape[:-1]:
+        raise ValueError("gate and beta must have shape q.shape[:-1]")
+    if gate.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise ValueError("gate and beta must be fp32")
+    if k.dtype != q.dtype or v.dtype != q.dtype or q.dtype not in _DTYPES:
+        raise ValueError("q, k, v must share one dtype, fp32 or bf16")
+    if not dense and cu_seqlens.dtype != torch.int32:
+        raise ValueError("cu_seqlens must be int32")
+    n = q.shape[0] if dense else cu_seqlens.numel() - 1
+    if initial_state is not None:
+        want = (n, q.shape[-2], v.shape[-1], q.shape[-1])
+        if tuple(initial_state.shape) != want or initial_state.dtype != torch.float32:
+            raise ValueError(f"initial_state must be fp32 {want}")
+    return n
+
+
+def prefill(q, k, v, g=None, beta=None, *, alpha=None, cu_seqlens=None, initial_state=None,
+            output_final_state=True, algo="auto", chunk=64, workspace=None, out=None,
+            final_state=None, stream=None):
+    """Gated delta-rule prefill.  Returns (o, final_state or None).
+
+    g is the per-token log-decay (alpha = exp(g)); pass alpha= instead to give
+    alpha itself.  ``initial_state=None`` starts from zeros.
+    """
+    gate, gate_kind = _gate(g, alpha)
+    n = _check_prefill_shapes(q, k, v, gate, beta, cu_seqlens, initial_state)
+    o = out if out is not None else torch.empty(v.shape, dtype=q.dtype, device=q.device)
+    fin = final_state
+    if fin is None and output_final_state:
+        fin = torch.empty((n, q.shape[-2], v.shape[-1], q.shape[-1]), dtype=torch.float32,
+                          device=q.device)
+    args = prefill_args(q, k, v, gate, beta, gate_kind, cu_seqlens, initial_state, fin, o, algo,
+                        chunk)
+    need = workspace_bytes(args)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if workspace is not None:
+        args.workspace, args.workspace_bytes = _ptr(workspace), workspace.numel()
+    _abi.check(_abi.lib().rhz_gdr_prefill(byref(args), _stream(stream)))
+    return o, fin
+
+
+def decode_args(q, k, v, gate, beta, gate_kind, state, o) -> _abi.DecodeArgs:
+    B, H, dk = q.shape
+    a = _abi.DecodeArgs()
+    a.batch, a.heads, a.d_k, a.d_v = B, H, dk, v.shape[-1]
+    a.dtype = _DTYPES[q.dtype]
+    a.gate_kind = gate_kind
+    a.q, a.k, a.v, a.gate, a.beta = _ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta)
+    a.state, a.o = _ptr(state), _ptr(o)
+    return a
+
+
+def decode_step(q, k, v, g=None, beta=None, *, alpha=None, state, out=None, stream=None):
+    """One decode position for every (b, h); ``state`` [B,H,d_v,d_k] fp32 is updated in place."""
+    gate, gate_kind = _gate(g, alpha)
+    B, H, dk = q.shape
+    dv = v.shape[-1]
+    if k.shape != q.shape or v.shape[:2] != (B, H) or gate.shape != (B, H) or beta.shape != (B, H):
+        raise ValueError("decode shapes: q,k [B,H,dk], v [B,H,dv], gate/beta [B,H]")
+    if tuple(state.shape) != (B, H, dv, dk) or state.dtype != torch.float32:
+        raise ValueError("state must be fp32 [B,H,d_v,d_k]")
+    o = out if out is not None else torch.empty((B, H, dv), dtype=q.dtype, device=q.device)
+    args = decode_args(q, k, v, gate, beta, gate_kind, state, o)
+    _abi.check(_abi.lib().rhz_gdr_decode_step(byref(args), _stream(stream)))
+    return o
+
+
+_FILL = {"normal": _abi.FILL_NORMAL, "unit_rows": _abi.FILL_UNIT_ROWS,
+         "sigmoid": _abi.FILL_SIGMOID, "neg_softplus": _abi.FILL_NEG_SOFTPLUS}
+_FILL_DTYPES = {torch.float64: _abi.F64, torch.float32: _abi.F32, torch.bfloat16: _abi.BF16}
+
+
+def philox_fill(kind: str, seed: int, stream_id: int, shape, dtype=torch.float32, *,
+                mean: float = 0.0, std: float = 1.0, device="cuda", out=None, stream=None):
+    """Seeded Philox-4x32-10 synthetic tensor generated on the device (see rhz_philox_fill)."""
+    t = out if out is not None else torch.empty(shape, dtype=dtype, device=device)
+    row_len = t.shape[-1] if t.dim() else 1
+    _abi.check(_abi.lib().rhz_philox_fill(_FILL[kind], seed, stream_id, t.numel(), row_len, mean,
+                                          std, _FILL_DTYPES[t.dtype], _ptr(t), _stream(stream)))
+    return t
+
+
+def query_support(op: str, dtype, d_k: int, d_v: int, algo: str = "auto") -> int:
+    """rhz_gdr_query_support status for op 'scan' or 'step'."""
+    ops = {"scan": _abi.OP_DELTA_SCAN, "step": _abi.OP_DELTA_STEP}
+    return _abi.lib().rhz_gdr_query_support(ops[op], _DTYPES[dtype], d_k, d_v, _ALGOS[algo])

@@ -1,0 +1,142 @@
+"""GPU parity of rhz_gdr_prefill (chunked bf16 MFMA path and recurrent fp32 path)
+against the f64 oracle on identical seeded inputs, through the C ABI.
+
+Reference behaviour followed: gated_delta_sequential / gated_delta_scan_chunked
+(crates/ops/src/delta.rs:133-197), batched and with the initial state honoured.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gdr_cases import BF16_TOL, C0, C1, C2, C4, F32_TOL, Prefill, check_close, varlen_lengths
+
+pytestmark = pytest.mark.gpu
+
+PATHS = [("chunked", torch.bfloat16, BF16_TOL), ("recurrent", torch.float32, F32_TOL),
+         ("recurrent", torch.bfloat16, BF16_TOL)]
+
+
+def _check(w, o, fin, tol, seqs=None, heads=None, tag=""):
+    ref_o, ref_f = w.oracle(seqs, heads)
+    o = o.float().cpu().numpy()
+    fin = fin.cpu().numpy()
+    if seqs is not None or heads is not None:
+        mask = ~np.isnan(ref_o)
+        mo = check_close(o[mask], ref_o[mask], tol, f"{tag} o")
+        fm = ~np.isnan(ref_f)
+        mf = check_close(fin[fm], ref_f[fm], tol, f"{tag} final state")
+    else:
+        mo = check_close(o, ref_o, tol, f"{tag} o")
+        mf = check_close(fin, ref_f, tol, f"{tag} final state")
+    print(f"{tag}: o {mo}  final {mf}", flush=True)
+    return mo, mf
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+def test_config0(device, algo, dtype, tol):
+    w = Prefill(**C0, dtype=dtype, device=device)
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"c0 {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+@pytest.mark.parametrize("shape", [
+    dict(batch=2, heads=3, seq_len=100, d_k=64, d_v=64),
+    dict(batch=1, heads=2, seq_len=1, d_k=128, d_v=128),
+    dict(batch=3, heads=1, seq_len=63, d_k=32, d_v=96),
+    dict(batch=1, heads=2, seq_len=200, d_k=128, d_v=256),
+    dict(batch=2, heads=2, seq_len=129, d_k=16, d_v=8),
+])
+def test_shapes(device, algo, dtype, tol, shape):
+    w = Prefill(**shape, dtype=dtype, device=device, state_std=0.02)
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"{shape} {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+def test_varlen_with_edges(device, algo, dtype, tol):
+    # empty, single-token, chunk-boundary and ragged sequences in one pack
+    lengths = [0, 1, 63, 64, 65, 200, 0, 130]
+    w = Prefill(heads=4, d_k=128, d_v=128, lengths=lengths, dtype=dtype, device=device,
+                state_std=0.02)
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"varlen edges {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+def test_alpha_gate_with_resets(device, algo, dtype, tol):
+    """gate given as alpha, with alpha = 0 at some positions (a reset, delta.rs:348-358)."""
+    w = Prefill(batch=2, heads=2, seq_len=150, d_k=64, d_v=64, dtype=dtype, device=device,
+                state_std=0.02)
+    alpha64 = np.exp(w.g64)
+    alpha64[0, :] = 0.0     # sequence start
+    alpha64[70, 1] = 0.0    # mid-chunk reset
+    alpha64[128, 0] = 0.0   # chunk-start reset
+    alpha64[155, :] = 0.0   # inside the second sequence
+    alpha_dev = torch.from_numpy(alpha64.astype(np.float32)).to(device)
+    w.alpha64 = alpha_dev.double().cpu().numpy()
+    import rhizome_amd
+    o, fin = rhizome_amd.prefill(w.shaped(w.q), w.shaped(w.k), w.shaped(w.v), None,
+                                 w.shaped(w.beta), alpha=w.shaped(alpha_dev),
+                                 initial_state=w.init, algo=algo)
+    torch.cuda.synchronize()
+    _check(w, o.reshape(w.n_tok, w.heads, w.d_v), fin, tol, tag=f"alpha gate {algo}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+@pytest.mark.parametrize("scale", [1e-4, 1e4])
+def test_value_magnitudes(device, algo, dtype, tol, scale):
+    """v and S0 scaled by 1e-4 / 1e4: the op is linear in (v, S0) jointly; the
+    chunked path's fp16 operands are rescaled by powers of two per chunk."""
+    w = Prefill(batch=2, heads=2, seq_len=200, d_k=128, d_v=64, dtype=dtype, device=device,
+                state_std=0.02)
+    w.v = (w.v.double() * scale).to(dtype)
+    w.v64 = w.v.double().cpu().numpy()
+    w.init = w.init * scale
+    w.init64 = w.init.double().cpu().numpy()
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"scale {scale} {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype", [("chunked", torch.bfloat16), ("recurrent", torch.float32)])
+def test_deterministic_and_batch_invariant(device, algo, dtype):
+    lengths = [300, 77, 640, 1, 129]
+    w = Prefill(heads=3, d_k=128, d_v=128, lengths=lengths, dtype=dtype, device=device,
+                state_std=0.02)
+    o1, f1 = w.run(algo=algo)
+    o2, f2 = w.run(algo=algo)
+    assert torch.equal(o1, o2) and torch.equal(f1, f2), "run-to-run results differ"
+    # sequence 2 alone must give bit-identical results to its slot in the pack
+    import rhizome_amd
+    a, b = int(w.cu[2]), int(w.cu[3])
+    cu = torch.tensor([0, b - a], dtype=torch.int32, device=device)
+    o3, f3 = rhizome_amd.prefill(w.q[a:b], w.k[a:b], w.v[a:b], w.g[a:b], w.beta[a:b],
+                                 cu_seqlens=cu, initial_state=w.init[2:3].contiguous(), algo=algo)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, o1[a:b]) and torch.equal(f3[0], f1[2]), "batch invariance broken"
+
+
+@pytest.mark.parametrize("algo,dtype,tol", [("chunked", torch.bfloat16, BF16_TOL),
+                                            ("recurrent", torch.float32, F32_TOL)])
+def test_config1_full(device, algo, dtype, tol):
+    """B=4 H=16 T=4096 d=128, every head against the oracle."""
+    w = Prefill(**C1, dtype=dtype, device=device)
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"c1 {algo}")
+
+
+def test_config2_long_context(device):
+    """B=1 H=32 T=32768 d_k=128 d_v=256, slow decay; heads 0, 13 and 31 against the oracle."""
+    w = Prefill(**C2, dtype=torch.bfloat16, device=device)
+    o, fin = w.run(algo="chunked")
+    _check(w, o, fin, BF16_TOL, seqs=[0], heads=[0, 13, 31], tag="c2 chunked")
+
+
+def test_config4_varlen(device):
+    """64 packed sequences, lengths U[128, 8192], init states; 24 (seq, head) units checked."""
+    lengths = varlen_lengths(C4["n_seqs"], C4["len_lo"], C4["len_hi"])
+    w = Prefill(heads=C4["heads"], d_k=C4["d_k"], d_v=C4["d_v"], lengths=lengths,
+                dtype=torch.bfloat16, device=device, state_std=C4["state_std"])
+    o, fin = w.run(algo="chunked")
+    longest = int(np.argmax(lengths))
+    _check(w, o, fin, BF16_TOL, seqs=[0, 7, longest, 63], heads=[0, 5, 15], tag="c4 chunked")
