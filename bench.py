@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Gated delta-rule benchmark on one MI355X (gfx950).
+
+Headline (the JSON line's `value`): chunked prefill throughput in tokens/s on
+B=4, H=16, T=4096, d_k=d_v=128, bf16 q/k/v, fp32 gates/state, chunk 64 --
+one step = one rhz_gdr_prefill over the whole batch (all heads), inputs
+resident in HBM.  Alongside (`decode`): the decode state update on B=256,
+H=16, d=128, fp32 state, one rhz_gdr_decode_step launch per step over 64
+steps, as HBM GB/s.
+
+Inputs are synthetic and seeded: the reference's Philox-4x32-10 streams
+(q=1, k=2, v=3, beta=4, g=5, state=6), generated on the device by
+rhz_philox_fill.  Timing uses HIP events on the stream the library launches
+on.  `roofline.achieved` counts algorithmic work only:
+  prefill flops per (chunk of c tokens, head): 6 c^2 d_k + 4 c^2 d_v + 6 c d_k d_v
+  decode bytes per (b, h): 8 d_k d_v + 4 (2 d_k + 2 d_v) + 8
+`cpu_baseline` times the f64 CPU oracle (a restatement of
+crates/ops/src/delta.rs) on this host in the same run.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GDR prefill tokens/s + decode state-update HBM GB/s on 1 MI355X"
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+PREFILL = dict(batch=4, heads=16, seq_len=4096, d_k=128, d_v=128, chunk=64)
+DECODE = dict(batch=256, heads=16, d_k=128, d_v=128, steps=64)
+
+
+def prefill_flops(lengths, heads, dk, dv, chunk=64) -> float:
+    total = 0
+    for n in lengths:
+        full, rem = divmod(int(n), chunk)
+        for c in [chunk] * full + ([rem] if rem else []):
+            total += 6 * c * c * dk + 4 * c * c * dv + 6 * c * dk * dv
+    return float(total * heads)
+
+
+def prefill_bytes(tokens, heads, dk, dv, n_seqs, e_in=2, e_out=2, init_state=False) -> float:
+    per_tok = (2 * dk + dv) * e_in + dv * e_out + 2 * 4
+    states = n_seqs * heads * dk * dv * 4 * (2 if init_state else 1)
+    return float(tokens * heads * per_tok + states)
+
+
+def decode_bytes(batch, heads, dk, dv) -> float:
+    return float(batch * heads * (2 * 4 * dk * dv + 4 * (2 * dk + 2 * dv) + 8))
+
+
+def traffic_from_profiles(kind: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters, from the
+    committed summary profiles/hbm_traffic.md (line `traffic <kind>: <bytes>`)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(rf"\s*traffic {kind}:\s*([0-9.eE+]+)", line)
+        if m:
+            return float(m.group(1))
+    return None
+
+
+def time_region(torch, stream, fn, reps: int) -> float:
+    """Milliseconds per call of fn over reps calls, HIP events on `stream`."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def bench_prefill(torch, steps, warmup):
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = PREFILL
+    B, T, H, dk, dv = c["batch"], c["seq_len"], c["heads"], c["d_k"], c["d_v"]
+    dev = torch.device("cuda:0")
+    bf16, f32 = torch.bfloat16, torch.float32
+    q = rhizome_amd.philox_fill("unit_rows", 0, 1, (B, T, H, dk), bf16)
+    k = rhizome_amd.philox_fill("unit_rows", 0, 2, (B, T, H, dk), bf16)
+    v = rhizome_amd.philox_fill("normal", 0, 3, (B, T, H, dv), bf16)
+    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, (B, T, H), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, (B, T, H), f32)
+    o = torch.empty((B, T, H, dv), dtype=bf16, device=dev)
+    fin = torch.empty((B, H, dv, dk), dtype=f32, device=dev)
+    args = gdr.prefill_args(q, k, v, g, beta, _abi.GATE_LOG_ALPHA, None, None, fin, o, "chunked")
+    ws = torch.empty(gdr.workspace_bytes(args), dtype=torch.uint8, device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    stream = torch.cuda.current_stream()
+    lib, argp, sp = _abi.lib(), ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream or None)
+
+    def step():
+        st = lib.rhz_gdr_prefill(argp, sp)
+        if st:
+            _abi.check(st)
+
+    for _ in range(warmup):
+        step()
+    ms = time_region(torch, stream, step, steps)
+    flops = prefill_flops([T] * B, H, dk, dv)
+    algo_bytes = prefill_bytes(B * T, H, dk, dv, B)
+    host = {"q": q, "k": k, "v": v, "g": g, "beta": beta}
+    return ms, flops, algo_bytes, host
+
+
+def bench_decode(torch, warmup):
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = DECODE
+    B, H, dk, dv, n = c["batch"], c["heads"], c["d_k"], c["d_v"], c["steps"]
+    f32 = torch.float32
+    q = rhizome_amd.philox_fill("unit_rows", 0, 1, (n, B, H, dk), f32)
+    k = rhizome_amd.philox_fill("unit_rows", 0, 2, (n, B, H, dk), f32)
+    v = rhizome_amd.philox_fill("normal", 0, 3, (n, B, H, dv), f32)
+    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, (n, B, H), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, (n, B, H), f32)
+    state = rhizome_amd.philox_fill("normal", 0, 6, (B, H, dv, dk), f32, std=0.02)
+    o = torch.empty((n, B, H, dv), dtype=f32, device=q.device)
+    lib = _abi.lib()
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream or None)
+    argv = [gdr.decode_args(q[t], k[t], v[t], g[t], beta[t], _abi.GATE_LOG_ALPHA, state, o[t])
+            for t in range(n)]
+    ptrs = [ctypes.byref(a) for a in argv]
+    count = [0]
+
+    def step():
+        st = lib.rhz_gdr_decode_step(ptrs[count[0] % n], sp)
+        count[0] += 1
+        if st:
+            _abi.check(st)
+
+    for _ in range(warmup):
+        step()
+    ms = time_region(torch, stream, step, n)
+    return ms, decode_bytes(B, H, dk, dv), {"q": q, "k": k, "v": v, "g": g, "beta": beta}
+
+
+def cpu_baseline(pre_host, dec_host):
+    """f64 oracle on this host: reference three-pass step with per-call allocations."""
+    import numpy as np
+    from oracle import oracle as O
+
+    cores = O.default_threads()
+    c = PREFILL
+    B, T, H, dk = c["batch"], c["seq_len"], c["heads"], c["d_k"]
+    # prefill: every (b, h) head of the workload, unit-major f64
+    q = pre_host["q"].double().cpu().numpy().transpose(0, 2, 1, 3).reshape(B * H, T, dk)
+    k = pre_host["k"].double().cpu().numpy().transpose(0, 2, 1, 3).reshape(B * H, T, dk)
+    v = pre_host["v"].double().cpu().numpy().transpose(0, 2, 1, 3).reshape(B * H, T, c["d_v"])
+    a = np.exp(pre_host["g"].double().cpu().numpy()).transpose(0, 2, 1).reshape(B * H, T)
+    b = pre_host["beta"].double().cpu().numpy().transpose(0, 2, 1).reshape(B * H, T)
+    t0 = time.perf_counter()
+    O.bench_sequential(q, k, v, a, b, threads=cores)
+    t_all = time.perf_counter() - t0
+    # single thread: two heads, scaled to the workload
+    t0 = time.perf_counter()
+    O.bench_sequential(q[:2], k[:2], v[:2], a[:2], b[:2], threads=1)
+    t_one = (time.perf_counter() - t0) / 2 * (B * H)
+    # decode: 8 steps of every (b, h) of the decode workload
+    d = DECODE
+    U = d["batch"] * d["heads"]
+    nst = 8
+    qd = dec_host["q"][:nst].double().cpu().numpy().reshape(nst, U, d["d_k"])
+    kd = dec_host["k"][:nst].double().cpu().numpy().reshape(nst, U, d["d_k"])
+    vd = dec_host["v"][:nst].double().cpu().numpy().reshape(nst, U, d["d_v"])
+    ad = np.exp(dec_host["g"][:nst].double().cpu().numpy()).reshape(nst, U)
+    bd = dec_host["beta"][:nst].double().cpu().numpy().reshape(nst, U)
+    S = np.zeros((U, d["d_v"], d["d_k"]))
+    t0 = time.perf_counter()
+    for s in range(nst):
+        O.bench_step(qd[s], kd[s], vd[s], ad[s], bd[s], S, threads=cores)
+    t_dec = (time.perf_counter() - t0) / nst
+    return {
+        "value": B * T / t_all,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"full prefill workload (B={B} H={H} T={T} d={dk}, {B * H} heads) through "
+                   "the f64 oracle's gated_delta_sequential, heads spread over all cores"),
+        "single_thread_value": B * T / t_one,
+        "cpu": _cpu_model(),
+        "decode": {"value": decode_bytes(d["batch"], d["heads"], d["d_k"], d["d_v"]) / t_dec / 1e9,
+                   "unit": "GB/s", "cores": cores,
+                   "sample": f"{nst} steps of gated_delta_step on all {U} (b,h) heads"},
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the gated delta-rule needs no collective and this "
+              "build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    ms, flops, algo_bytes, pre_host = bench_prefill(torch, args.steps, args.warmup)
+    dms, dbytes, dec_host = bench_decode(torch, args.warmup)
+    c = PREFILL
+    tokens = c["batch"] * c["seq_len"]
+    achieved = flops / (ms * 1e-3) / 1e12
+    traffic = traffic_from_profiles("prefill")
+    dgbs = dbytes / (dms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": tokens / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Philox-4x32-10 on the device)",
+        "config": {"workload": "chunked GDR prefill", "batch": c["batch"], "heads": c["heads"],
+                   "seq_len": c["seq_len"], "d_k": c["d_k"], "d_v": c["d_v"], "chunk": c["chunk"],
+                   "inputs": "bf16 q/k/v, fp32 log-decay and beta", "state": "fp32",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": traffic,
+                     "kernel": "gdr_chunk_prep_kernel<128> + gdr_chunk_scan_kernel<128>",
+                     "flops_per_launch": flops, "algorithmic_bytes": algo_bytes,
+                     "launch_us": ms * 1e3},
+        "decode": {"metric": "decode state-update HBM GB/s", "value": dgbs, "unit": "GB/s",
+                   "ms_per_step": dms, "steps": DECODE["steps"],
+                   "config": {"workload": "GDR decode step, state in place", **DECODE,
+                              "dtype": "fp32"},
+                   "roofline": {"bound": "hbm", "achieved": dgbs, "peak": PEAK_HBM_GBS,
+                                "unit": "GB/s", "frac": dgbs / PEAK_HBM_GBS,
+                                "traffic": traffic_from_profiles("decode"),
+                                "kernel": "gdr_decode_kernel<8,4,true,float>",
+                                "bytes_per_launch": dbytes, "launch_us": dms * 1e3}},
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(pre_host, dec_host)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

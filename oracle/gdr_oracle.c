@@ -458,3 +458,48 @@ int orc_max_threads(void)
     return 1;
 #endif
 }
+
+/* ------------------------------------------------------------------ */
+/* CPU baseline timing (bench.py cpu_baseline leg)                     */
+/* ------------------------------------------------------------------ */
+
+/* gated_delta_sequential (delta.rs:133-154, with its per-step allocations)
+ * over n_units independent heads stored unit-major ([unit][T][d] for q, k,
+ * v; [unit][T] for alpha, beta), nthreads-way parallel over units.  Outputs
+ * go to out [unit][T][d] and final [unit][d][d]. */
+void orc_bench_sequential(int64_t n_units, int64_t t_len, int64_t d, const double* q,
+                          const double* k, const double* v, const double* alpha,
+                          const double* beta, double* out, double* final_state, int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+    for (int64_t u = 0; u < n_units; ++u) {
+        uint64_t* seg = (uint64_t*)calloc((size_t)(t_len > 0 ? t_len : 1), sizeof(uint64_t));
+        double* init = (double*)calloc((size_t)(d * d), sizeof(double));
+        orc_gated_delta_sequential(t_len, d, q + u * t_len * d, k + u * t_len * d,
+                                   v + u * t_len * d, alpha + u * t_len, beta + u * t_len, seg,
+                                   init, out + u * t_len * d, final_state + u * d * d);
+        free(init);
+        free(seg);
+    }
+}
+
+/* gated_delta_step (delta.rs:94-127) once for each of n_units heads:
+ * q, k, v [unit][d], alpha, beta [unit], state [unit][d][d] in place. */
+void orc_bench_step(int64_t n_units, int64_t d, const double* q, const double* k, const double* v,
+                    const double* alpha, const double* beta, double* state, double* o,
+                    int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t u = 0; u < n_units; ++u) {
+        double* r = orc_gated_delta_step(state + u * d * d, d, q + u * d, k + u * d, v + u * d,
+                                         alpha[u], beta[u]);
+        memcpy(o + u * d, r, (size_t)d * sizeof(double));
+        free(r);
+    }
+}

@@ -72,6 +72,9 @@ def lib():
         L.orc_gdr_decode_batched.argtypes = [
             c_int64, c_int64, c_int64, c_int64, _dp, _dp, _dp, _dp, _dp, _dp, _dp, c_int]
         L.orc_max_threads.restype = c_int
+        L.orc_bench_sequential.argtypes = [c_int64, c_int64, c_int64, _dp, _dp, _dp, _dp, _dp,
+                                           _dp, _dp, c_int]
+        L.orc_bench_step.argtypes = [c_int64, c_int64, _dp, _dp, _dp, _dp, _dp, _dp, _dp, c_int]
         _lib = L
     return _lib
 
@@ -318,3 +321,26 @@ def gdr_inputs(n_tok: int, heads: int, dk: int, dv: int, seed: int = 0, g_mean: 
         out["state"] = philox_normal(seed, STREAM["state"], n_state * heads * dv * dk, 0.0,
                                      state_std).reshape(n_state, heads, dv, dk)
     return out
+
+
+# ------------------------------------------------------- CPU baseline timing
+def bench_sequential(q, k, v, alpha, beta, threads: int):
+    """gated_delta_sequential over independent heads: q,k,v [U,T,d], alpha,beta [U,T]."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    alpha, beta = _f64(alpha), _f64(beta)
+    u, t, d = q.shape
+    out = np.zeros((u, t, d))
+    fin = np.zeros((u, d, d))
+    lib().orc_bench_sequential(u, t, d, _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out),
+                               _p(fin), threads)
+    return out, fin
+
+
+def bench_step(q, k, v, alpha, beta, state: np.ndarray, threads: int):
+    """gated_delta_step once per head: q,k,v [U,d], alpha,beta [U], state [U,d,d] in place."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    alpha, beta = _f64(alpha), _f64(beta)
+    u, d = q.shape
+    o = np.zeros((u, d))
+    lib().orc_bench_step(u, d, _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(state), _p(o), threads)
+    return o

@@ -1,0 +1,195 @@
+"""The C ABI of librhizome_gdr.so without a GPU: the library loads, exports
+every function include/rhizome_gdr.h declares, and every validation error is
+returned (with its detail message) before any HIP call is made."""
+import ctypes
+import subprocess
+from ctypes import byref, c_size_t
+
+import pytest
+
+from rhizome_amd import _abi
+
+A = 0x10000  # a 256-byte-aligned fake device address; never dereferenced
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.lib()
+
+
+def test_exports_every_declared_function(lib):
+    declared = _abi.declared_functions()
+    assert len(declared) >= 8
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [f for f in declared if f not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for f in declared:
+        assert hasattr(lib, f)
+
+
+def test_identity_and_status_strings(lib):
+    assert lib.rhz_gdr_abi_version() == 1
+    names = {0: "RHZ_OK", 1: "RHZ_ERR_INVALID_ARG", 2: "RHZ_ERR_UNSUPPORTED",
+             3: "RHZ_ERR_WORKSPACE", 4: "RHZ_ERR_HIP", 99: "RHZ_ERR_UNKNOWN"}
+    for code, name in names.items():
+        assert _abi.status_string(code) == name
+
+
+@pytest.mark.parametrize("op,dtype,dk,dv,algo,want", [
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 128, 128, _abi.ALGO_CHUNKED, _abi.OK),
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 128, 256, _abi.ALGO_AUTO, _abi.OK),
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 64, 64, _abi.ALGO_CHUNKED, _abi.OK),
+    (_abi.OP_DELTA_SCAN, _abi.F32, 128, 128, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 100, 128, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 256, 128, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_SCAN, _abi.BF16, 6, 6, _abi.ALGO_AUTO, _abi.OK),
+    (_abi.OP_DELTA_SCAN, _abi.F32, 256, 1024, _abi.ALGO_RECURRENT, _abi.OK),
+    (_abi.OP_DELTA_SCAN, _abi.F32, 257, 64, _abi.ALGO_RECURRENT, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_STEP, _abi.F32, 128, 128, _abi.ALGO_AUTO, _abi.OK),
+    (_abi.OP_DELTA_STEP, _abi.F32, 128, 128, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_STEP, _abi.F32, 128, 2048, _abi.ALGO_AUTO, _abi.ERR_UNSUPPORTED),
+    (7, _abi.F32, 128, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
+    (_abi.OP_DELTA_STEP, _abi.F64, 128, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
+    (_abi.OP_DELTA_STEP, _abi.F32, 0, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
+    (_abi.OP_DELTA_SCAN, _abi.F32, 128, 128, 9, _abi.ERR_INVALID_ARG),
+])
+def test_query_support(lib, op, dtype, dk, dv, algo, want):
+    assert lib.rhz_gdr_query_support(op, dtype, dk, dv, algo) == want
+
+
+def _prefill(**over):
+    a = _abi.PrefillArgs()
+    a.batch, a.seq_len, a.heads, a.d_k, a.d_v, a.chunk = 4, 4096, 16, 128, 128, 64
+    a.dtype, a.gate_kind, a.algo = _abi.BF16, _abi.GATE_LOG_ALPHA, _abi.ALGO_AUTO
+    for name in ("q", "k", "v", "gate", "beta", "o", "final_state"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+def _ws(a):
+    n = c_size_t(0)
+    st = _abi.lib().rhz_gdr_prefill_workspace_size(byref(a), byref(n))
+    return st, n.value
+
+
+def test_workspace_sizes():
+    st, n = _ws(_prefill())
+    assert st == _abi.OK
+    slots, heads = 4 * 64, 16
+    expected = 256 + 256 + ((slots * heads * 8 + 255) // 256) * 256 + slots * heads * 16384
+    assert n == expected
+    assert _ws(_prefill(dtype=_abi.F32)) == (_abi.OK, 0)
+    assert _ws(_prefill(algo=_abi.ALGO_RECURRENT)) == (_abi.OK, 0)
+    assert _ws(_prefill(d_k=100))[1] == 0  # AUTO falls back to the recurrent path
+    st, n = _ws(_prefill(cu_seqlens=A, batch=64, seq_len=266000))
+    assert st == _abi.OK and n > (266000 // 64) * 16 * 16384
+    assert _ws(_prefill(seq_len=0)) == (_abi.OK, 1024 - 512)  # headers only
+    assert _abi.lib().rhz_gdr_prefill_workspace_size(byref(_prefill()), None) == _abi.ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(batch=0), _abi.ERR_INVALID_ARG, "batch"),
+    (dict(seq_len=-1), _abi.ERR_INVALID_ARG, "seq_len"),
+    (dict(heads=0), _abi.ERR_INVALID_ARG, "heads"),
+    (dict(d_k=0), _abi.ERR_INVALID_ARG, "d_k"),
+    (dict(d_v=0), _abi.ERR_INVALID_ARG, "d_v"),
+    (dict(chunk=0), _abi.ERR_INVALID_ARG, "chunk"),
+    (dict(dtype=_abi.F64), _abi.ERR_INVALID_ARG, "dtype"),
+    (dict(gate_kind=5), _abi.ERR_INVALID_ARG, "gate_kind"),
+    (dict(algo=-1), _abi.ERR_INVALID_ARG, "algo"),
+    (dict(d_k=300), _abi.ERR_UNSUPPORTED, "d_k"),
+    (dict(d_v=2000), _abi.ERR_UNSUPPORTED, "d_v"),
+    (dict(dtype=_abi.F32, algo=_abi.ALGO_CHUNKED), _abi.ERR_UNSUPPORTED, "bf16"),
+    (dict(d_k=100, algo=_abi.ALGO_CHUNKED), _abi.ERR_UNSUPPORTED, "multiples of 8"),
+    (dict(batch=70000, seq_len=70000), _abi.ERR_INVALID_ARG, "2^31"),
+    (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
+    (dict(k=None), _abi.ERR_INVALID_ARG, "k is NULL"),
+    (dict(v=None), _abi.ERR_INVALID_ARG, "v is NULL"),
+    (dict(gate=None), _abi.ERR_INVALID_ARG, "gate is NULL"),
+    (dict(beta=None), _abi.ERR_INVALID_ARG, "beta is NULL"),
+    (dict(o=None), _abi.ERR_INVALID_ARG, "o is NULL"),
+    (dict(q=A + 8), _abi.ERR_INVALID_ARG, "16-byte aligned"),
+    (dict(final_state=A + 4), _abi.ERR_INVALID_ARG, "final_state"),
+    (dict(dtype=_abi.F32, algo=_abi.ALGO_RECURRENT, v=A + 2), _abi.ERR_INVALID_ARG, "v is not aligned"),
+    (dict(beta=A + 1), _abi.ERR_INVALID_ARG, "4-byte aligned"),
+    (dict(), _abi.ERR_WORKSPACE, "workspace is NULL"),
+    (dict(workspace=A, workspace_bytes=1024), _abi.ERR_WORKSPACE, "needed"),
+])
+def test_prefill_validation(over, status, msg):
+    args = _prefill(**over)
+    st = _abi.lib().rhz_gdr_prefill(byref(args), None)
+    assert st == status, _abi.last_error()
+    assert msg in _abi.last_error()
+
+
+def test_prefill_workspace_alignment():
+    st, need = _ws(_prefill())
+    args = _prefill(workspace=A + 16, workspace_bytes=need)
+    assert _abi.lib().rhz_gdr_prefill(byref(args), None) == _abi.ERR_WORKSPACE
+    assert "256-byte" in _abi.last_error()
+    assert _abi.lib().rhz_gdr_prefill(None, None) == _abi.ERR_INVALID_ARG
+
+
+def _decode(**over):
+    a = _abi.DecodeArgs()
+    a.batch, a.heads, a.d_k, a.d_v = 256, 16, 128, 128
+    a.dtype, a.gate_kind = _abi.F32, _abi.GATE_LOG_ALPHA
+    for name in ("q", "k", "v", "gate", "beta", "state", "o"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(batch=0), _abi.ERR_INVALID_ARG, "batch"),
+    (dict(heads=-3), _abi.ERR_INVALID_ARG, "heads"),
+    (dict(d_k=0), _abi.ERR_INVALID_ARG, "d_k"),
+    (dict(d_v=0), _abi.ERR_INVALID_ARG, "d_v"),
+    (dict(dtype=7), _abi.ERR_INVALID_ARG, "dtype"),
+    (dict(gate_kind=2), _abi.ERR_INVALID_ARG, "gate_kind"),
+    (dict(d_k=512), _abi.ERR_UNSUPPORTED, "256"),
+    (dict(d_v=4096), _abi.ERR_UNSUPPORTED, "1024"),
+    (dict(state=None), _abi.ERR_INVALID_ARG, "state is NULL"),
+    (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
+    (dict(o=None), _abi.ERR_INVALID_ARG, "o is NULL"),
+    (dict(k=A + 2), _abi.ERR_INVALID_ARG, "k is not aligned"),
+    (dict(state=A + 2), _abi.ERR_INVALID_ARG, "4-byte aligned"),
+])
+def test_decode_validation(over, status, msg):
+    args = _decode(**over)
+    assert _abi.lib().rhz_gdr_decode_step(byref(args), None) == status
+    assert msg in _abi.last_error()
+    assert _abi.lib().rhz_gdr_decode_step(None, None) == _abi.ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((9, 0, 1, 10, 1, 0.0, 1.0, _abi.F32, A), "kind"),
+    ((0, 0, 1, -1, 1, 0.0, 1.0, _abi.F32, A), "count"),
+    ((0, 0, 1, 10, 1, 0.0, 1.0, 5, A), "out_dtype"),
+    ((1, 0, 1, 10, 3, 0.0, 1.0, _abi.F32, A), "row_len"),
+    ((1, 0, 1, 10, 0, 0.0, 1.0, _abi.F32, A), "row_len"),
+    ((0, 0, 1, 10, 1, 0.0, 1.0, _abi.F32, None), "out is NULL"),
+])
+def test_philox_fill_validation(args, msg):
+    assert _abi.lib().rhz_philox_fill(*args, None) == _abi.ERR_INVALID_ARG
+    assert msg in _abi.last_error()
+
+
+def test_python_front_end_rejects_host_tensors():
+    import torch
+
+    import rhizome_amd
+
+    q = torch.zeros((1, 4, 2, 8), dtype=torch.bfloat16)
+    g = torch.zeros((1, 4, 2))
+    with pytest.raises(ValueError):
+        rhizome_amd.prefill(q, q, q, g, g)
+    with pytest.raises(ValueError):
+        rhizome_amd.prefill(q, q, q[..., :4, :], g, g)
+    with pytest.raises(ValueError):
+        rhizome_amd.prefill(q, q, q, g, g, alpha=g)
