@@ -258,7 +258,7 @@ def main() -> int:
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": traffic,
-                     "kernel": "gdr_chunk_prep_kernel<128> + gdr_chunk_scan_kernel<128>",
+                     "kernel": "gdr_chunk_kernel<128>",
                      "flops_per_launch": flops, "algorithmic_bytes": algo_bytes,
                      "launch_us": ms * 1e3},
         "decode": {"metric": "decode state-update HBM GB/s", "value": dgbs, "unit": "GB/s",

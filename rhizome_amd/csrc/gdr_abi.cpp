@@ -163,11 +163,13 @@ rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (algo == RHZ_ALGO_CHUNKED) {
         const size_t need = rhz::chunked_workspace_bytes(*args);
-        if (!args->workspace) return fail(RHZ_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", need);
-        if (args->workspace_bytes < need)
-            return fail(RHZ_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", args->workspace_bytes, need);
-        if (reinterpret_cast<uintptr_t>(args->workspace) & 255u)
-            return fail(RHZ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+        if (need) {
+            if (!args->workspace) return fail(RHZ_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", need);
+            if (args->workspace_bytes < need)
+                return fail(RHZ_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", args->workspace_bytes, need);
+            if (reinterpret_cast<uintptr_t>(args->workspace) & 255u)
+                return fail(RHZ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+        }
         return hip_status(rhz::launch_chunked(*args, st), "chunked prefill launch");
     }
     return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");

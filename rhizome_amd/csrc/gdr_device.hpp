@@ -51,11 +51,26 @@ __device__ __forceinline__ float exp2i(int e) {
 // floor(log2(m)) for a positive normal float m (-127 for zero/subnormal).
 __device__ __forceinline__ int ilog2f(float m) { return int((__float_as_uint(m) >> 23) & 0xffu) - 127; }
 
-// Maximum over the 64 lanes of a wave (every lane receives it).
+// Cross-lane move within rows of 16 lanes (DPP); lanes without a source read 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
+// Maximum over the 64 lanes of a wave, returned to every lane: DPP within
+// rows of 16 (quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), then the
+// four row maxima through scalar registers.
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
-    return x;
+    x = fmaxf(x, dpp_mov<0xB1>(x));
+    x = fmaxf(x, dpp_mov<0x4E>(x));
+    x = fmaxf(x, dpp_mov<0x124>(x));
+    x = fmaxf(x, dpp_mov<0x128>(x));
+    const int xi = __builtin_bit_cast(int, x);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // Element loads of the two input dtypes, widened to float.

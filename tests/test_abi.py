@@ -77,17 +77,13 @@ def _ws(a):
 
 
 def test_workspace_sizes():
-    st, n = _ws(_prefill())
-    assert st == _abi.OK
-    slots, heads = 4 * 64, 16
-    expected = 256 + 256 + ((slots * heads * 8 + 255) // 256) * 256 + slots * heads * 16384
-    assert n == expected
+    # dense batches need none; packed batches hold the longest-first order of the sequences
+    assert _ws(_prefill()) == (_abi.OK, 0)
     assert _ws(_prefill(dtype=_abi.F32)) == (_abi.OK, 0)
-    assert _ws(_prefill(algo=_abi.ALGO_RECURRENT)) == (_abi.OK, 0)
-    assert _ws(_prefill(d_k=100))[1] == 0  # AUTO falls back to the recurrent path
-    st, n = _ws(_prefill(cu_seqlens=A, batch=64, seq_len=266000))
-    assert st == _abi.OK and n > (266000 // 64) * 16 * 16384
-    assert _ws(_prefill(seq_len=0)) == (_abi.OK, 1024 - 512)  # headers only
+    assert _ws(_prefill(algo=_abi.ALGO_RECURRENT, cu_seqlens=A)) == (_abi.OK, 0)
+    assert _ws(_prefill(cu_seqlens=A, batch=64, seq_len=266000)) == (_abi.OK, 256)
+    assert _ws(_prefill(cu_seqlens=A, batch=65, seq_len=266000)) == (_abi.OK, 512)
+    assert _ws(_prefill(d_k=100, cu_seqlens=A)) == (_abi.OK, 0)  # AUTO falls back to recurrent
     assert _abi.lib().rhz_gdr_prefill_workspace_size(byref(_prefill()), None) == _abi.ERR_INVALID_ARG
 
 
@@ -116,8 +112,8 @@ def test_workspace_sizes():
     (dict(final_state=A + 4), _abi.ERR_INVALID_ARG, "final_state"),
     (dict(dtype=_abi.F32, algo=_abi.ALGO_RECURRENT, v=A + 2), _abi.ERR_INVALID_ARG, "v is not aligned"),
     (dict(beta=A + 1), _abi.ERR_INVALID_ARG, "4-byte aligned"),
-    (dict(), _abi.ERR_WORKSPACE, "workspace is NULL"),
-    (dict(workspace=A, workspace_bytes=1024), _abi.ERR_WORKSPACE, "needed"),
+    (dict(cu_seqlens=A), _abi.ERR_WORKSPACE, "workspace is NULL"),
+    (dict(cu_seqlens=A, workspace=A, workspace_bytes=16), _abi.ERR_WORKSPACE, "needed"),
 ])
 def test_prefill_validation(over, status, msg):
     args = _prefill(**over)
@@ -127,8 +123,8 @@ def test_prefill_validation(over, status, msg):
 
 
 def test_prefill_workspace_alignment():
-    st, need = _ws(_prefill())
-    args = _prefill(workspace=A + 16, workspace_bytes=need)
+    st, need = _ws(_prefill(cu_seqlens=A))
+    args = _prefill(cu_seqlens=A, workspace=A + 16, workspace_bytes=need)
     assert _abi.lib().rhz_gdr_prefill(byref(args), None) == _abi.ERR_WORKSPACE
     assert "256-byte" in _abi.last_error()
     assert _abi.lib().rhz_gdr_prefill(None, None) == _abi.ERR_INVALID_ARG
