@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -71,6 +72,10 @@ rhz_status check_prefill(const rhz_gdr_prefill_args* a, bool check_ptrs, int* al
             return fail(RHZ_ERR_UNSUPPORTED,
                         "CHUNKED needs d_k in 8..128 and d_v >= 8, both multiples of 8 (got d_k=%d d_v=%d)",
                         a->d_k, a->d_v);
+        // The kernel addresses one 64-token chunk of a head with 32-bit byte offsets.
+        if ((int64_t)a->heads * std::max(a->d_k, a->d_v) * 2 * 64 > kMaxIndex)
+            return fail(RHZ_ERR_UNSUPPORTED, "CHUNKED needs heads * max(d_k, d_v) below 2^24 (got %lld)",
+                        (long long)a->heads * std::max(a->d_k, a->d_v));
     }
     *algo_out = algo;
     if (!check_ptrs) return ok();

@@ -18,47 +18,66 @@
 // One workgroup of 8 waves per (sequence, head, 32 rows of S).  Rows of S
 // are independent, so the d_v split is exact, and each of the two "scan"
 // waves owns 16 whole rows of S (every key column) in fp32 MFMA
-// accumulators.  All four state-dependent GEMMs of a chunk (X = [K;Q] S0^T,
-// U = T R, O = gamma X_Q + P U, S^T += K^T Uhat) run on 16x16x32 fp16 MFMA
-// with the B operand taken straight from the wave's own accumulators: MFMA
-// row m of block b stands for index tok(b, m), chosen so that an
-// accumulator lane holds 8 consecutive indices of each block pair -- exactly
-// the contraction slots of the next product.  So the state-dependent chain
-// never leaves the wave; the transposed K operand comes from
-// ds_read_b64_tr_b16.
+// accumulators.  All four state-dependent GEMMs of a chunk (X = K S0^T,
+// O^T = (Q S0^T)^T + U^T P^T, U = T R, S^T += K^T Uhat) run on 16x16x32 fp16
+// MFMA with the state-side operand taken straight from the wave's own
+// registers: MFMA row m of block b stands for index tok(b, m), chosen so
+// that an accumulator lane holds 8 consecutive indices of each block pair --
+// exactly the operand slots of the next product.  So the state-dependent
+// chain never leaves the wave; the transposed K operand comes from
+// ds_read_b64_tr_b16, and O is produced transposed, so that each lane stores
+// 4 consecutive outputs of one token.
 //
 // The other six waves prepare the state-independent data one chunk ahead,
 // in lockstep with two barriers per chunk:
 //   interval A: scan X, R  |  T's off-diagonal 16x16 blocks of chunk c
-//               (waves 2, 3)  |  K, Q, V, gates of chunk c+1 into LDS from
-//               registers, and chunk c+2 into registers (waves 4-7);
-//   interval B: scan U, O, S update  |  K K^T and Q K^T of chunk c+1
-//               (waves 2, 3, 6, 7) into A and P, and T's diagonal 16x16
-//               blocks by forward substitution in fp32 registers.
+//               (waves 2, 3)  |  K, Q, beta V and the gates of chunk c+1 into
+//               LDS from registers, and chunk c+2 into registers (waves 4-7);
+//   interval B: scan U, O, S update  |  for chunk c+1: K K^T's diagonal
+//               blocks and T's diagonal blocks by forward substitution
+//               (wave 2), K K^T below the diagonal (wave 3), Q K^T (waves
+//               4-7).
 // T = (I + A)^-1 is blocked forward substitution: diagonal blocks by
-// substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.
+// substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.  The chunk loop
+// is unrolled by two, so that the double-buffer index is a compile-time
+// constant and every LDS address is a per-lane base plus an immediate.
 //
 // Operand precision: every GEMM runs on fp16 MFMA (11-bit significands)
 // with fp32 accumulation; the carried state is fp32.  K and Q are the bf16
-// inputs converted exactly to fp16 (q, k are L2-normalised rows, delta.rs:
-// 17-20, so |q.k| <= |q| stays far inside fp16 range); |T| <= 1 for unit
-// keys and beta in [0, 1].  S0, R, U and Uhat, whose magnitudes follow the
-// data, are rescaled by one power of two per chunk and wave (eS from
-// max|S|, eR from max|R|) and the scale is undone exactly in fp32.
+// inputs converted to fp16 (exact for |x| >= 2^-14; q, k are L2-normalised
+// rows, delta.rs:17-20, so |q.k| <= |q| stays far inside fp16 range);
+// |T| <= 1 for unit keys and beta in [0, 1].  The state is held as
+// S = Stilde 2^F with one exponent F per scan wave; R, U and O are computed
+// in the same scale.  F moves by a power of two only when max|Stilde| or
+// max|Rtilde| leaves a window that keeps the fp16 operands (Stilde, Rtilde,
+// U) far from overflow and underflow, so in steady state no rescaling
+// multiply is executed, and every scale change is exact.
+
+#include <utility>
 
 #include "gdr_device.hpp"
 #include "gdr_internal.hpp"
+
+#ifndef RHZ_TRACE_POINT
+#define RHZ_TRACE_POINT(chunk, slot) ((void)0)
+#endif
 
 namespace rhz {
 namespace {
 
 constexpr int kTV = 32;           // rows of S per workgroup (two scan waves of 16)
 constexpr int kMaxSortSeqs = 4096;
-constexpr int kMaxScaleExp = 60;  // bound on the power-of-two operand scales
-constexpr int kLDT = 72;          // fp16 row stride of 64-wide LDS tiles
+constexpr int kMaxScaleExp = 60;  // bound on one rescaling step
+constexpr int kMaxStateExp = 96;  // bound on the state exponent F
+constexpr int kLDT = 64;          // fp16 row stride of the 64x64 tiles A, T, P
+constexpr int kLDV = 68;          // fp32 row stride of the beta V tile
+constexpr int kLDD = 20;          // fp32 row stride of A's diagonal blocks
+constexpr int kGateWave = 3;      // loader wave (of 4) that processes the gates
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct ChunkParams {
@@ -75,6 +94,45 @@ struct ChunkParams {
     int batch, seq_len, heads, d_k, d_v, gate_is_alpha;
     int n_tiles;  // ceil(d_v / 32)
 };
+
+// LDS tile addressing.  Rows are unpadded and the 16-byte chunks of a row
+// are permuted by an XOR with a GF(2)-linear function of the row index.  The
+// functions were chosen by measuring this kernel's access patterns on gfx950
+// (MFMA operand reads of rows tok(b, 0..15) and 16t + 0..15 at a 16-byte
+// column, transposed 8-byte reads of K^T and T, and the staging and epilogue
+// writes) over candidate permutations: with them the 16-byte operand reads
+// run at the LDS's full rate, where padded rows or the identity permutation
+// lose a factor of two to bank conflicts.  Reads never straddle a chunk.
+__device__ __forceinline__ int rbit(int r, int i) { return (r >> i) & 1; }
+
+template <int DK>
+struct KQ;  // K and Q tiles: 64 tokens x DK key columns, fp16
+template <>
+struct KQ<128> {
+    static constexpr int LD = 128;
+    static __device__ __forceinline__ int off(int r, int j) {
+        const int f = (4 * rbit(r, 0)) ^ (14 * rbit(r, 1)) ^ (3 * rbit(r, 2)) ^ (12 * rbit(r, 3)) ^ (2 * rbit(r, 5));
+        return r * LD + (((j >> 3) ^ f) << 3) + (j & 7);
+    }
+};
+template <>
+struct KQ<64> {
+    static constexpr int LD = 64;
+    static __device__ __forceinline__ int off(int r, int j) {
+        const int f = 2 * rbit(r, 3) | 4 * (rbit(r, 4) ^ rbit(r, 2));
+        return r * LD + (((j >> 3) ^ f) << 3) + (j & 7);
+    }
+};
+template <>
+struct KQ<32> {
+    static constexpr int LD = 40;  // padded by one chunk
+    static __device__ __forceinline__ int off(int r, int j) { return r * LD + (((j >> 3) ^ (2 * rbit(r, 4))) << 3) + (j & 7); }
+};
+// A, T, P tiles: 64 x 64, fp16
+__device__ __forceinline__ int toff(int r, int s) {
+    const int f = (3 * rbit(r, 0)) ^ rbit(r, 1) ^ (3 * rbit(r, 2)) ^ (6 * rbit(r, 3)) ^ (3 * rbit(r, 4)) ^ (7 * rbit(r, 5));
+    return r * kLDT + (((s >> 3) ^ f) << 3) + (s & 7);
+}
 
 __device__ __forceinline__ f16x8 ld_f16x8(const uint16_t* p) {
     return __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(p));
@@ -93,7 +151,16 @@ __device__ __forceinline__ f32x4 mfma16x32h(f16x8 a, f16x8 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mfma16x16h(f16x4 a, f16x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f16x8 pack8(f32x4 lo, f32x4 hi, float s) {
+__device__ __forceinline__ f16x8 pack8(f32x4 lo, f32x4 hi) {
+    f16x8 r;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        r[v] = (_Float16)lo[v];
+        r[4 + v] = (_Float16)hi[v];
+    }
+    return r;
+}
+__device__ __forceinline__ f16x8 pack8s(f32x4 lo, f32x4 hi, float s) {
     f16x8 r;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -102,15 +169,31 @@ __device__ __forceinline__ f16x8 pack8(f32x4 lo, f32x4 hi, float s) {
     }
     return r;
 }
+__device__ __forceinline__ uint2 pack_bf16x4(f32x4 a) {
+    bf16x4 r;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) r[v] = (__bf16)a[v];  // round to nearest even
+    return __builtin_bit_cast(uint2, r);
+}
+__device__ __forceinline__ uint2 pack_f16x4(f32x4 a) {
+    f16x4 r;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) r[v] = (_Float16)a[v];
+    return __builtin_bit_cast(uint2, r);
+}
+__device__ __forceinline__ f32x4 ld_f32x4(const float* p) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    return (f32x4){x.x, x.y, x.z, x.w};
+}
 
-// Eight bf16 values -> eight fp16 values (exact for |x| in the fp16 normal range).
+// Two bf16 (one dword) -> two fp16, round to nearest even (exact for
+// |x| >= 2^-14 and below the fp16 maximum).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {
+    const f16x2 r = {(_Float16)__uint_as_float(u << 16), (_Float16)__uint_as_float(u & 0xffff0000u)};
+    return __builtin_bit_cast(uint32_t, r);
+}
 __device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 u) {
-    uint4 r;
-    r.x = pack_f16x2(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u));
-    r.y = pack_f16x2(__uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
-    r.z = pack_f16x2(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u));
-    r.w = pack_f16x2(__uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u));
-    return r;
+    return make_uint4(bf16x2_to_f16x2(u.x), bf16x2_to_f16x2(u.y), bf16x2_to_f16x2(u.z), bf16x2_to_f16x2(u.w));
 }
 
 // Index (token of a chunk, or key column) carried by MFMA row m of 16-row
@@ -130,14 +213,31 @@ __device__ __forceinline__ void seq_bounds(const int* cu, int seq, int seq_len, 
     }
 }
 
-// Chunk-local cumulative log-decay (wave-wide inclusive scan over the 64 tokens).
-__device__ __forceinline__ float chunk_cumsum(float g, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(g, off, kWave);
-        if (lane >= off) g += y;
-    }
-    return g;
+// Inclusive prefix sum over the 64 lanes of a wave: shifts within rows of
+// 16 lanes, then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then rows 0-1's total into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ float wave_incl_scan(float x) {
+    x += dpp_mov<0x111>(x);
+    x += dpp_mov<0x112>(x);
+    x += dpp_mov<0x114>(x);
+    x += dpp_mov<0x118>(x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xa, 0xf, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xc, 0xf, false));
+    return x;
+}
+__device__ __forceinline__ float lane_val(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Power-of-two rescaling step for a quantity whose maximum magnitude is m
+// (wave-uniform): 0 while floor(log2 m) lies in [lo, hi) or m is 0, else
+// the shift that brings the maximum to [2^target, 2^(target+1)), limited so
+// that the state exponent F + shift stays within +-kMaxStateExp.
+__device__ __forceinline__ int rescale_shift(float m, int lo, int hi, int target, int F) {
+    const int e = ilog2f(m);
+    if (!(m > 0.f) || (e >= lo && e < hi)) return 0;
+    const int s = min(max(e - target, -kMaxScaleExp), kMaxScaleExp);
+    return min(max(F + s, -kMaxStateExp), kMaxStateExp) - F;
 }
 
 // ------------------------------------------------------------ varlen setup
@@ -188,198 +288,676 @@ __device__ __forceinline__ void map_block(int bid, int units, int nt, int& unit,
 // whole kernel.
 template <int DK>
 struct Smem {
-    static constexpr int LDK = DK + 8;  // fp16 row stride of K/Q tiles
-    uint16_t k[2][64 * LDK];            // [buf][token][col], fp16
-    uint16_t q[2][64 * LDK];
-    uint16_t t[2][64 * kLDT];           // T, row-major fp16
-    uint16_t p[2][64 * kLDT];           // P, row-major fp16
-    uint16_t a[64 * kLDT];              // A, row-major fp16
-    uint16_t vt[2][kTV * kLDT];         // V tile transposed [state row][token], bf16
-    float gcum[2][64], gam[2][64], gdl[2][64], bs[2][64];
+    uint16_t k[2][64 * KQ<DK>::LD];  // [buf] token x key column, fp16
+    uint16_t q[2][64 * KQ<DK>::LD];
+    uint16_t t[2][64 * kLDT];        // T
+    uint16_t p[2][64 * kLDT];        // P
+    uint16_t a[64 * kLDT];           // A, blocks below the diagonal
+    float ad[4 * 16 * kLDD];         // A, diagonal 16x16 blocks, fp32
+    float vb[2][kTV * kLDV];         // beta_s v_s[i], [state row i][token s]
+    float gcum[2][64];               // G_s
+    float gam[2][64];                // exp(G_s)
+    float gdl[2][64];                // exp(G_last - G_s)
+    float nbg[2][64];                // -beta_s exp(G_s)
+    float bs[2][64];                 // beta_s
+    float dst[2][64];                // exp(G_s - G_{16 floor(s/16)})
+    float den[2][64];                // exp(G_{16 floor(s/16) + 15} - G_s)
+    float pf[2][16];                 // [4 bi + bj]: exp(G_{16 bi} - G_{16 bj + 15}), bi > bj
 };
 
+// Per-workgroup constants shared by the roles.
+struct Unit {
+    int h, seq, tb, te, nch, i0;
+};
+
+// ------------------------------------------------------------ loader waves
 // Registers holding one chunk's inputs between its load and its staging
 // (loader waves 4-7, lt = thread index within them).
 template <int DK>
 struct ChunkIn {
     uint4 k[DK / 32], q[DK / 32];  // 16-byte pieces of K and Q rows
-    uint4 v;                       // 8 values of the V tile
+    uint4 v;                       // 8 values of the V tile (token lt / 4)
     float g, b;                    // gate and beta of token lt % 64
+    float bv;                      // beta of token lt / 4
 };
 
-// Loads are unconditional (indices clamped into the sequence and the row);
-// out-of-range values are zeroed when staged.
+// Byte offsets of a loader lane's pieces relative to the first token of a
+// chunk (row = token within the chunk, clamped to last).
 template <int DK>
-__device__ __forceinline__ void load_chunk(const ChunkParams& p, int h, int tb, int te, int i0, int c, int lt,
-                                           ChunkIn<DK>& r) {
-    constexpr int PPR = DK / 8;
-    const int t0 = tb + c * kChunk, last = min(kChunk, te - t0) - 1;
-    const int H = p.heads, dk = p.d_k;
+struct LoadOffsets {
+    uint32_t kq[DK / 32], v, g, bv;
+    __device__ void set(const ChunkParams& p, int i0, int lt, int last) {
+        constexpr int PPR = DK / 8;
+        const uint32_t H = p.heads, dk = p.d_k, dv = p.d_v;
 #pragma unroll
-    for (int u = 0; u < DK / 32; ++u) {
-        const int it = lt + 256 * u, row = min(it / PPR, last), c8 = min((it % PPR) * 8, dk - 8);
-        const long off = ((long)(t0 + row) * H + h) * dk + c8;
-        r.k[u] = *reinterpret_cast<const uint4*>(p.k + off);
-        r.q[u] = *reinterpret_cast<const uint4*>(p.q + off);
+        for (int u = 0; u < DK / 32; ++u) {
+            const int it = lt + 256 * u, row = min(it / PPR, last), c8 = min((it % PPR) * 8, p.d_k - 8);
+            kq[u] = (uint32_t(row) * H * dk + c8) * 2u;
+        }
+        const int vrow = min(lt >> 2, last);
+        v = (uint32_t(vrow) * H * dv + uint32_t(min(i0 + (lt & 3) * 8, p.d_v - 8) - i0)) * 2u;
+        g = uint32_t(min(lt & 63, last)) * H * 4u;
+        bv = uint32_t(vrow) * H * 4u;
     }
-    {
-        const int row = min(lt >> 2, last), c8 = min(i0 + (lt & 3) * 8, p.d_v - 8);
-        r.v = *reinterpret_cast<const uint4*>(p.v + ((long)(t0 + row) * H + h) * p.d_v + c8);
-    }
-    const long gi = (long)(t0 + min(lt & 63, last)) * H + h;
-    r.g = p.gate[gi];
-    r.b = p.beta[gi];
-}
+};
 
 template <int DK>
-__device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, int tb, int te, int i0, int c,
-                                            int lt, const ChunkIn<DK>& r) {
-    constexpr int PPR = DK / 8, LDK = Smem<DK>::LDK;
-    const int t0 = tb + c * kChunk, len = min(kChunk, te - t0), b = c & 1;
-    const uint4 z = make_uint4(0, 0, 0, 0);
+__device__ __forceinline__ void load_chunk(const ChunkParams& p, const Unit& u, int c, const LoadOffsets<DK>& o,
+                                           ChunkIn<DK>& r) {
+    const size_t t0 = size_t(u.tb) + size_t(c) * kChunk;
+    const size_t H = p.heads;
+    const char* kb = reinterpret_cast<const char*>(p.k + (t0 * H + u.h) * p.d_k);
+    const char* qb = reinterpret_cast<const char*>(p.q + (t0 * H + u.h) * p.d_k);
+    const char* vb = reinterpret_cast<const char*>(p.v + (t0 * H + u.h) * p.d_v + u.i0);
+    const char* gb = reinterpret_cast<const char*>(p.gate + t0 * H + u.h);
+    const char* bb = reinterpret_cast<const char*>(p.beta + t0 * H + u.h);
 #pragma unroll
-    for (int u = 0; u < DK / 32; ++u) {
-        const int it = lt + 256 * u, row = it / PPR, c8 = (it % PPR) * 8;
-        const bool ok = row < len && c8 < p.d_k;
-        *reinterpret_cast<uint4*>(&sm.k[b][row * LDK + c8]) = ok ? bf16x8_to_f16x8(r.k[u]) : z;
-        *reinterpret_cast<uint4*>(&sm.q[b][row * LDK + c8]) = ok ? bf16x8_to_f16x8(r.q[u]) : z;
+    for (int i = 0; i < DK / 32; ++i) {
+        r.k[i] = *reinterpret_cast<const uint4*>(kb + o.kq[i]);
+        r.q[i] = *reinterpret_cast<const uint4*>(qb + o.kq[i]);
     }
-    {
+    r.v = *reinterpret_cast<const uint4*>(vb + o.v);
+    r.g = *reinterpret_cast<const float*>(gb + o.g);
+    r.b = *reinterpret_cast<const float*>(bb + o.g);
+    r.bv = *reinterpret_cast<const float*>(bb + o.bv);
+}
+
+// Loads chunk c; the offsets of a partial last chunk are clamped.
+template <int DK>
+__device__ __forceinline__ void load_chunk_any(const ChunkParams& p, const Unit& u, int c, const LoadOffsets<DK>& full,
+                                               int lt, ChunkIn<DK>& r) {
+    const int len = min(kChunk, u.te - (u.tb + c * kChunk));
+    if (len == kChunk) {
+        load_chunk<DK>(p, u, c, full, r);
+    } else {
+        LoadOffsets<DK> o;
+        o.set(p, u.i0, lt, len - 1);
+        load_chunk<DK>(p, u, c, o, r);
+    }
+}
+
+template <int DK, int NB>
+__device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, int s, int len, const ChunkIn<DK>& r) {
+    const float g = s < len ? log_decay(r.g, p.gate_is_alpha) : 0.f;
+    const float beta = s < len ? r.b : 0.f;
+    const float G = wave_incl_scan(g);
+    const float Glast = lane_val(G, 63);
+    const float B0 = lane_val(G, 0), B1 = lane_val(G, 16), B2 = lane_val(G, 32), B3 = lane_val(G, 48);
+    const float E0 = lane_val(G, 15), E1 = lane_val(G, 31), E2 = lane_val(G, 47);
+    const int blk = s >> 4;
+    const float Gs = blk == 0 ? B0 : blk == 1 ? B1 : blk == 2 ? B2 : B3;
+    const float Ge = blk == 0 ? E0 : blk == 1 ? E1 : blk == 2 ? E2 : Glast;
+    const float gam = __expf(G);
+    sm.gcum[NB][s] = G;
+    sm.gam[NB][s] = gam;
+    sm.gdl[NB][s] = __expf(Glast - G);
+    sm.nbg[NB][s] = -beta * gam;
+    sm.bs[NB][s] = beta;
+    sm.dst[NB][s] = __expf(G - Gs);
+    sm.den[NB][s] = __expf(Ge - G);
+    if (s < 16) {
+        const int bi = s >> 2, bj = s & 3;
+        const float gi = bi == 0 ? B0 : bi == 1 ? B1 : bi == 2 ? B2 : B3;
+        const float gj = bj == 0 ? E0 : bj == 1 ? E1 : bj == 2 ? E2 : Glast;
+        sm.pf[NB][s] = bi > bj ? __expf(gi - gj) : 0.f;
+    }
+}
+
+// Chunk inputs from registers into LDS buffer NB: K and Q as fp16, beta V
+// transposed, and (GATES: the gate wave) the gates.  Out-of-range rows and columns are
+// written as zeros.
+template <int DK, int NB, bool GATES>
+__device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, int len, int i0, int lt,
+                                            const ChunkIn<DK>& r) {
+    constexpr int PPR = DK / 8;
+    const bool full = len == kChunk && p.d_k == DK && i0 + kTV <= p.d_v;  // uniform
+    if (full) {
+#pragma unroll
+        for (int u = 0; u < DK / 32; ++u) {
+            const int it = lt + 256 * u, row = it / PPR, c8 = (it % PPR) * 8;
+            *reinterpret_cast<uint4*>(&sm.k[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8(r.k[u]);
+            *reinterpret_cast<uint4*>(&sm.q[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8(r.q[u]);
+        }
         const int row = lt >> 2, c8 = (lt & 3) * 8;
-        const uint4 v = (row < len && i0 + c8 < p.d_v) ? r.v : z;
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t wv[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            sm.vt[b][(c8 + 2 * e) * kLDT + row] = uint16_t(wv[e]);
-            sm.vt[b][(c8 + 2 * e + 1) * kLDT + row] = uint16_t(wv[e] >> 16);
+            sm.vb[NB][(c8 + 2 * e) * kLDV + row] = r.bv * __uint_as_float(wv[e] << 16);
+            sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = r.bv * __uint_as_float(wv[e] & 0xffff0000u);
+        }
+    } else {
+        const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < DK / 32; ++u) {
+            const int it = lt + 256 * u, row = it / PPR, c8 = (it % PPR) * 8;
+            const bool ok = row < len && c8 < p.d_k;
+            *reinterpret_cast<uint4*>(&sm.k[NB][KQ<DK>::off(row, c8)]) = ok ? bf16x8_to_f16x8(r.k[u]) : z;
+            *reinterpret_cast<uint4*>(&sm.q[NB][KQ<DK>::off(row, c8)]) = ok ? bf16x8_to_f16x8(r.q[u]) : z;
+        }
+        const int row = lt >> 2, c8 = (lt & 3) * 8;
+        const bool ok = row < len && i0 + c8 < p.d_v;
+        const uint32_t wv[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sm.vb[NB][(c8 + 2 * e) * kLDV + row] = ok ? r.bv * __uint_as_float(wv[e] << 16) : 0.f;
+            sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = ok ? r.bv * __uint_as_float(wv[e] & 0xffff0000u) : 0.f;
         }
     }
-    if (lt < 64) {  // one wave: gates of the 64 tokens
-        const float g = lt < len ? log_decay(r.g, p.gate_is_alpha) : 0.f;
-        const float G = chunk_cumsum(g, lt);
-        const float Glast = __shfl(G, 63, kWave);
-        sm.gcum[b][lt] = G;
-        sm.gam[b][lt] = __expf(G);
-        sm.gdl[b][lt] = __expf(Glast - G);
-        sm.bs[b][lt] = lt < len ? r.b : 0.f;
-    }
+    if constexpr (GATES) stage_gates<DK, NB>(p, sm, lt & 63, len, r);
 }
 
-// T_ij = -T_ii (sum_{m=j}^{i-1} A_im T_mj) for one 16x16 block of the
-// row-major T in tt, by one wave (16x16x16 MFMA).  T_mj enters as the B
-// operand through a transposed read.
+// ------------------------------------------------------------ K K^T, Q K^T
+// Scheduling hints: the next n DS reads, MFMAs, ... go into one group.
+#define RHZ_SCHED_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
+
+// Rows 16 blk + 0..15 of a K or Q tile as the 16-byte operand slices of
+// lane (n, g): columns 32 ks + 8 g .. + 7.
 template <int DK>
-__device__ __forceinline__ void t_block(Smem<DK>& sm, uint16_t* tt, int i, int j, int l) {
-    const int n = l & 15, kg = l >> 4;
-    f32x4 y = {0.f, 0.f, 0.f, 0.f};
-    for (int m = j; m < i; ++m) {
-        const f16x4 a = ld_f16x4(&sm.a[(16 * i + n) * kLDT + 16 * m + 4 * kg]);
-        const s16x4 bt = ld_tr(&tt[(16 * m + 4 * kg + (n >> 2)) * kLDT + 16 * j + 4 * (n & 3)]);
-        y = mfma16x16h(a, __builtin_bit_cast(f16x4, bt), y);
-    }
-    // y[v] = Y[4*kg + v][n]: exactly the B operand of T_ii * Y.
-    f16x4 yb;
+__device__ __forceinline__ void load_rows(const uint16_t* src, int blk, int n, int g, f16x8* dst) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) yb[v] = (_Float16)y[v];
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    t = mfma16x16h(ld_f16x4(&tt[(16 * i + n) * kLDT + 16 * i + 4 * kg]), yb, t);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) tt[(16 * i + 4 * kg + v) * kLDT + 16 * j + n] = f32_to_f16(-t[v]);
+    for (int ks = 0; ks < DK / 32; ++ks) dst[ks] = ld_f16x8(&src[KQ<DK>::off(16 * blk + n, 32 * ks + 8 * g)]);
 }
 
-// K K^T (isQ false) or Q K^T rows rows_a, rows_b of 16-row blocks for chunk
-// buffer b: A (strictly lower) or P (lower incl.) with decay and beta applied.
-template <int DK>
-__device__ __forceinline__ void kk_rows(Smem<DK>& sm, int b, bool isQ, int ra, int rb, int l) {
-    constexpr int LDK = Smem<DK>::LDK, NK = DK / 32;
+// One 16x16 block (BI, BJ), BJ <= BI, of K K^T (ISQ false) or Q K^T for
+// chunk buffer NB, formed transposed, out^T = K_BJ Y_BI^T, so that lane
+// (n, g) holds out[16 BI + n][16 BJ + 4 g + 0..3].  xk holds the K rows of
+// block BJ, y the rows of block BI of K or Q.  Off-diagonal blocks go to A
+// (beta and decay applied) or P (decay applied) in fp16; the decay is the
+// product of three factors <= 1, exp(G_r - G_{16 BI}) exp(G_{16 BI} -
+// G_{16 BJ + 15}) exp(G_{16 BJ + 15} - G_s).  Diagonal blocks are masked to
+// s < r (A, kept in fp32 for the substitution) or s <= r (P).
+template <int DK, int NB, bool ISQ, int BI, int BJ>
+__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l) {
+    constexpr int NK = DK / 32;
+    constexpr bool diag = BI == BJ;
     const int n = l & 15, g = l >> 4;
-    const uint16_t* src = isQ ? sm.q[b] : sm.k[b];
-    f16x8 fa[NK], fb[NK];
+    const int r = 16 * BI + n, s0 = 16 * BJ + 4 * g;
+    // Epilogue factors, read before the products.
+    const float br = ISQ ? 1.f : sm.bs[NB][r];
+    const float Gr = sm.gcum[NB][r];
+    const float fr = diag ? 0.f : sm.dst[NB][r] * sm.pf[NB][4 * BI + BJ];
+    const f32x4 es = ld_f32x4(diag ? &sm.gcum[NB][s0] : &sm.den[NB][s0]);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) {
-        fa[ks] = ld_f16x8(&src[(16 * ra + n) * LDK + 32 * ks + 8 * g]);
-        fb[ks] = ld_f16x8(&src[(16 * rb + n) * LDK + 32 * ks + 8 * g]);
-    }
-    const float4 ga = *reinterpret_cast<const float4*>(&sm.gcum[b][16 * ra + 4 * g]);
-    const float4 gb = *reinterpret_cast<const float4*>(&sm.gcum[b][16 * rb + 4 * g]);
-    const float4 ba = *reinterpret_cast<const float4*>(&sm.bs[b][16 * ra + 4 * g]);
-    const float4 bb = *reinterpret_cast<const float4*>(&sm.bs[b][16 * rb + 4 * g]);
-    const float gra[4] = {ga.x, ga.y, ga.z, ga.w}, grb[4] = {gb.x, gb.y, gb.z, gb.w};
-    const float bra[4] = {ba.x, ba.y, ba.z, ba.w}, brb[4] = {bb.x, bb.y, bb.z, bb.w};
-    uint16_t* dst = isQ ? sm.p[b] : sm.a;
+    for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(xk[ks], y[ks], acc);
+    f32x4 x;
+    if constexpr (!diag) {
+        const float f = fr * br;
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
-        if (bj > rb) break;
-        const float gs = sm.gcum[b][16 * bj + n];
-        const int s = 16 * bj + n;
-        f16x8 fk[NK];
+        for (int v = 0; v < 4; ++v) x[v] = acc[v] * f * es[v];
+        *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = pack_f16x4(x);
+    } else {
 #pragma unroll
-        for (int ks = 0; ks < NK; ++ks) fk[ks] = ld_f16x8(&sm.k[b][(16 * bj + n) * LDK + 32 * ks + 8 * g]);
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int bi = half ? rb : ra;
-            if (bj > bi) continue;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(half ? fb[ks] : fa[ks], fk[ks], acc);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = 16 * bi + 4 * g + v;
-                const float d = __expf(fminf((half ? grb[v] : gra[v]) - gs, 0.f));
-                float x = d * acc[v];
-                if (!isQ) x *= half ? brb[v] : bra[v];
-                const bool keep = isQ ? (s <= r) : (s < r);
-                dst[r * kLDT + s] = f32_to_f16(keep ? x : 0.f);
-            }
+        for (int v = 0; v < 4; ++v) {
+            const int s = s0 + v;
+            const bool keep = ISQ ? (s <= r) : (s < r);
+            x[v] = keep ? acc[v] * br * __expf(Gr - es[v]) : 0.f;
         }
+        if constexpr (ISQ)
+            *reinterpret_cast<uint2*>(&sm.p[NB][toff(r, s0)]) = pack_f16x4(x);
+        else
+            *reinterpret_cast<float4*>(&sm.ad[(16 * BI + n) * kLDD + 4 * g]) = make_float4(x[0], x[1], x[2], x[3]);
     }
 }
 
-// Diagonal block blk of T = (I + A)^-1 by forward substitution: lane col
-// (0..15) solves column col in fp32 registers.
-template <int DK>
-__device__ __forceinline__ void t_diag(Smem<DK>& sm, uint16_t* tt, int blk, int col) {
-    float arow[16][16];
+// a from lane R of each row of 16 lanes (DPP row_newbcast) times t, and the
+// same added to acc: one VALU instruction each.  a is only ever written by LDS
+// loads, so the DPP source needs no wait states.
+template <int R>
+__device__ __forceinline__ float bcast_mul(float a, float t) {
+    float r;
+    asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(a), "v"(t), "i"(R));
+    return r;
+}
+template <int R>
+__device__ __forceinline__ float bcast_fma(float a, float t, float acc) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(a), "v"(t), "i"(R));
+    return acc;
+}
+// Row R of the forward substitution: t_R = -sum_{s<R} A[R][s] t_s, A[R][s]
+// broadcast from the lane that holds row R.
+template <int R>
+__device__ __forceinline__ void t_diag_row(float* t, const float* a, int col) {
+    float acc = bcast_mul<R>(a[0], t[0]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) {
-        const uint4 u0 = *reinterpret_cast<const uint4*>(&sm.a[(16 * blk + r) * kLDT + 16 * blk]);
-        const uint4 u1 = *reinterpret_cast<const uint4*>(&sm.a[(16 * blk + r) * kLDT + 16 * blk + 8]);
-        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    for (int s = 1; s < R; ++s) acc = bcast_fma<R>(a[s], t[s], acc);
+    if (R > col) t[R] = -acc;
+}
+template <int... R>
+__device__ __forceinline__ void t_diag_rows(float* t, const float* a, int col, std::integer_sequence<int, R...>) {
+    (t_diag_row<R + 1>(t, a, col), ...);
+}
+
+// Diagonal blocks of T = (I + A)^-1 by forward substitution in fp32, one
+// wave: lane 16 blk + col holds row col of A's diagonal block blk and solves
+// column col of T's.
+template <int DK, int NB>
+__device__ __forceinline__ void t_diag(Smem<DK>& sm, int l) {
+    const int blk = l >> 4, col = l & 15;
+    float a[16];
 #pragma unroll
-        for (int s = 0; s < 16; ++s)
-            arow[r][s] = float(__builtin_bit_cast(_Float16, uint16_t(w[s >> 1] >> (16 * (s & 1)))));
+    for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4 x = ld_f32x4(&sm.ad[(16 * blk + col) * kLDD + 4 * q4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * q4 + e] = x[e];
     }
     float t[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) t[r] = r == col ? 1.f : 0.f;
+    t_diag_rows(t, a, col, std::make_integer_sequence<int, 15>{});
 #pragma unroll
-    for (int r = 1; r < 16; ++r) {
-        float acc = 0.f;
+    for (int r = 0; r < 16; ++r) sm.t[NB][toff(16 * blk + r, 16 * blk + col)] = f32_to_f16(t[r]);
+}
+
+// T_ij = -T_ii (sum_{m=j}^{i-1} A_im T_mj) for one 16x16 block of T (buffer
+// NB), by one wave (16x16x16 MFMA).  Y = sum A_im T_mj takes T_mj through a
+// transposed read; the second product is formed transposed, (T_ii Y)^T =
+// Y^T T_ii^T, so that each lane writes 4 consecutive entries of one row.
+template <int DK, int NB, int I, int J>
+__device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
+    const int n = l & 15, kg = l >> 4;
+    uint16_t* tt = sm.t[NB];
+    f16x4 a[I - J];
+    s16x4 bt[I - J];
 #pragma unroll
-        for (int s = 0; s < r; ++s) acc += arow[r][s] * t[s];
-        if (r > col) t[r] = -acc;
+    for (int m = J; m < I; ++m) {
+        a[m - J] = ld_f16x4(&sm.a[toff(16 * I + n, 16 * m + 4 * kg)]);
+        bt[m - J] = ld_tr(&tt[toff(16 * m + 4 * kg + (n >> 2), 16 * J + 4 * (n & 3))]);
     }
+    const f16x4 tii = ld_f16x4(&tt[toff(16 * I + n, 16 * I + 4 * kg)]);
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) tt[(16 * blk + r) * kLDT + 16 * blk + col] = f32_to_f16(t[r]);
+    for (int m = J; m < I; ++m) y = mfma16x16h(a[m - J], __builtin_bit_cast(f16x4, bt[m - J]), y);
+    // y[v] = Y[4 kg + v][n]: the A operand Y^T of the transposed product.
+    f16x4 ya;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ya[v] = (_Float16)y[v];
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    t = mfma16x16h(ya, tii, t);
+    // t[v] = (T_ii Y)[n][4 kg + v]
+    *reinterpret_cast<uint2*>(&tt[toff(16 * I + n, 16 * J + 4 * kg)]) = pack_f16x4(-t);
+}
+
+// ------------------------------------------------------------ prep roles
+// Wave 2, interval A: T_10, T_20, T_30 of chunk buffer B; interval B: K K^T
+// diagonal blocks and T's diagonal blocks of buffer 1 - B.
+template <int DK, int B>
+__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, const Unit& u, int c, int l) {
+    constexpr int NB = 1 - B;
+    if (c >= 0) {
+        t_block<DK, B, 1, 0>(sm, l);
+        lds_fence();
+        t_block<DK, B, 2, 0>(sm, l);
+        lds_fence();
+        t_block<DK, B, 3, 0>(sm, l);
+    }
+    RHZ_TRACE_POINT(c, 0);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 1);
+    if (c + 1 < u.nch) {
+        constexpr int NK = DK / 32;
+        const int n = l & 15, g = l >> 4;
+        f16x8 kr[4][NK];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[NB], blk, n, g, kr[blk]);
+        kq_block<DK, NB, false, 0, 0>(sm, kr[0], kr[0], l);
+        kq_block<DK, NB, false, 1, 1>(sm, kr[1], kr[1], l);
+        kq_block<DK, NB, false, 2, 2>(sm, kr[2], kr[2], l);
+        kq_block<DK, NB, false, 3, 3>(sm, kr[3], kr[3], l);
+        lds_fence();
+        t_diag<DK, NB>(sm, l);
+    }
+    RHZ_TRACE_POINT(c, 2);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 3);
+}
+
+// Wave 3, interval A: T_32, T_21, T_31 of buffer B; interval B: K K^T below
+// the diagonal of buffer 1 - B.
+template <int DK, int B>
+__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, const Unit& u, int c, int l) {
+    constexpr int NB = 1 - B;
+    if (c >= 0) {
+        t_block<DK, B, 3, 2>(sm, l);
+        t_block<DK, B, 2, 1>(sm, l);
+        lds_fence();
+        t_block<DK, B, 3, 1>(sm, l);
+    }
+    RHZ_TRACE_POINT(c, 0);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 1);
+    if (c + 1 < u.nch) {
+        constexpr int NK = DK / 32;
+        const int n = l & 15, g = l >> 4;
+        f16x8 kr[4][NK];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[NB], blk, n, g, kr[blk]);
+        kq_block<DK, NB, false, 1, 0>(sm, kr[0], kr[1], l);
+        kq_block<DK, NB, false, 2, 0>(sm, kr[0], kr[2], l);
+        kq_block<DK, NB, false, 3, 0>(sm, kr[0], kr[3], l);
+        kq_block<DK, NB, false, 2, 1>(sm, kr[1], kr[2], l);
+        kq_block<DK, NB, false, 3, 1>(sm, kr[1], kr[3], l);
+        kq_block<DK, NB, false, 3, 2>(sm, kr[2], kr[3], l);
+    }
+    RHZ_TRACE_POINT(c, 2);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 3);
+}
+
+// Q K^T blocks of loader wave LW (0..3) for buffer NB:
+//   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)   LW 3: (3,1) (3,2) (3,3)
+template <int DK, int NB, int LW>
+__device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
+    constexpr int NK = DK / 32;
+    const int n = l & 15, g = l >> 4;
+    f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
+    if constexpr (LW == 0) {
+        load_rows<DK>(sm.k[NB], 0, n, g, x0);
+        load_rows<DK>(sm.q[NB], 0, n, g, y0);
+        load_rows<DK>(sm.q[NB], 1, n, g, y1);
+        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l);
+        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l);
+    } else if constexpr (LW == 1) {
+        load_rows<DK>(sm.k[NB], 1, n, g, x0);
+        load_rows<DK>(sm.q[NB], 1, n, g, y0);
+        load_rows<DK>(sm.q[NB], 2, n, g, y1);
+        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l);
+        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l);
+    } else if constexpr (LW == 2) {
+        load_rows<DK>(sm.k[NB], 0, n, g, x0);
+        load_rows<DK>(sm.q[NB], 2, n, g, y0);
+        load_rows<DK>(sm.q[NB], 3, n, g, y1);
+        load_rows<DK>(sm.k[NB], 2, n, g, x1);
+        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l);
+        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l);
+        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l);
+    } else {
+        load_rows<DK>(sm.q[NB], 3, n, g, y0);
+        load_rows<DK>(sm.k[NB], 1, n, g, x0);
+        load_rows<DK>(sm.k[NB], 2, n, g, x1);
+        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l);
+        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l);
+        load_rows<DK>(sm.k[NB], 3, n, g, x0);
+        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l);
+    }
+}
+
+// Loader waves 4-7, interval A: stage chunk c+1 into buffer 1 - B, load
+// chunk c+2; interval B: Q K^T of chunk c+1.
+template <int DK, int B, int LW>
+__device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int c, int lt,
+                                            const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
+    constexpr int NB = 1 - B;
+    const int nx = c + 1;
+    if (nx < u.nch) {
+        const int len = min(kChunk, u.te - (u.tb + nx * kChunk));
+        stage_chunk<DK, NB, LW == kGateWave>(p, sm, len, u.i0, lt, in);
+        load_chunk_any<DK>(p, u, min(nx + 1, u.nch - 1), lo, lt, in);
+    }
+    RHZ_TRACE_POINT(c, 0);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 1);
+    if (nx < u.nch) qk_blocks<DK, NB, LW>(sm, lt & 63);
+    RHZ_TRACE_POINT(c, 2);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 3);
+}
+
+template <int DK, int LW>
+__device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int lt) {
+    LoadOffsets<DK> lo;
+    lo.set(p, u.i0, lt, kChunk - 1);
+    ChunkIn<DK> in;
+    if (u.nch > 0) load_chunk_any<DK>(p, u, 0, lo, lt, in);
+    for (int c = -1; c < u.nch; c += 2) {
+        prep_loader<DK, 1, LW>(p, sm, u, c, lt, lo, in);
+        if (c + 1 < u.nch) prep_loader<DK, 0, LW>(p, sm, u, c + 1, lt, lo, in);
+    }
+}
+
+// ------------------------------------------------------------ scan waves
+template <int DK>
+struct ScanState {
+    f32x4 S[DK / 16];  // S[jb][v] = Stilde[i][tok(jb, 4g + v)],  S = Stilde 2^F
+    int F;
+    float smax;
+};
+
+template <int DK>
+__device__ __forceinline__ float state_max(const ScanState<DK>& st) {
+    float m = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < DK / 16; ++jb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(st.S[jb][v]));
+    return wave_max(m);
+}
+
+// One chunk of a scan wave (w = 0, 1) on buffer B.
+template <int DK, int B>
+__device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int c, int w, int l,
+                                           ScanState<DK>& st) {
+    constexpr int NK = DK / 32;  // 32-wide contraction steps over d_k
+    constexpr int NJ = DK / 16;  // 16-row blocks of key columns
+    const int n = l & 15, g = l >> 4;
+    const int il = 16 * w + n;
+    const int orow = u.i0 + 16 * w + 4 * g;  // first of the 4 output rows of this lane
+    const int H = p.heads, dv = p.d_v;
+    const bool act = c >= 0;
+    const int t0 = u.tb + c * kChunk, len = min(kChunk, u.te - t0);
+    // ---- interval A: X_K = K Stilde^T -> Rtilde;  O^T <- (Q Stilde^T)^T.
+    f32x4 OQ[4];
+    f16x8 Br[2];
+    int er = 0;
+    if (act) {
+        // Operands of this interval, read ahead of their products.
+        f16x8 kx[4][NK];
+#pragma unroll
+        for (int bk = 0; bk < 4; ++bk)
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) kx[bk][ks] = ld_f16x8(&sm.k[B][KQ<DK>::off(tok(bk, n), 32 * ks + 8 * g)]);
+        const int es = rescale_shift(st.smax, -12, 14, 13, st.F);
+        if (es != 0) {
+            const float f = exp2i(-es);
+#pragma unroll
+            for (int jb = 0; jb < NJ; ++jb) st.S[jb] *= f;
+            st.F += es;
+        }
+        f16x8 Bx[NK];
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) Bx[ks] = pack8(st.S[2 * ks], st.S[2 * ks + 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        // X_K on MFMA while the Q operands are read.
+        f16x8 qx[4][NK];
+#pragma unroll
+        for (int tb2 = 0; tb2 < 4; ++tb2)
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) qx[tb2][ks] = ld_f16x8(&sm.q[B][KQ<DK>::off(16 * tb2 + n, 32 * ks + 8 * g)]);
+        f32x4 XK[4];
+#pragma unroll
+        for (int bk = 0; bk < 4; ++bk) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(kx[bk][ks], Bx[ks], acc);
+            XK[bk] = acc;
+        }
+#pragma unroll
+        for (int it = 0; it < 4 * NK; ++it) {
+            RHZ_SCHED_GROUP(kSchedDsRead, 1);
+            RHZ_SCHED_GROUP(kSchedMfma, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 vv[4], nbg[4];
+        float gq[4];
+#pragma unroll
+        for (int bk = 0; bk < 4; ++bk) {
+            const int s0 = 32 * (bk >> 1) + 8 * g + 4 * (bk & 1);
+            vv[bk] = ld_f32x4(&sm.vb[B][il * kLDV + s0]);
+            nbg[bk] = ld_f32x4(&sm.nbg[B][s0]);
+            gq[bk] = sm.gam[B][16 * bk + n];
+        }
+        // (Q Stilde^T)^T on MFMA while Rtilde = beta V 2^-F - beta gamma X_K
+        // is formed.
+#pragma unroll
+        for (int tb2 = 0; tb2 < 4; ++tb2) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(Bx[ks], qx[tb2][ks], acc);
+            OQ[tb2] = acc;
+        }
+        RHZ_TRACE_POINT(c, 8);
+        float rmax = 0.f;
+        if (st.F == 0) {
+#pragma unroll
+            for (int bk = 0; bk < 4; ++bk)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float r = fmaf(nbg[bk][v], XK[bk][v], vv[bk][v]);
+                    XK[bk][v] = r;
+                    rmax = fmaxf(rmax, fabsf(r));
+                }
+        } else {
+            const float sv = exp2i(-st.F);
+#pragma unroll
+            for (int bk = 0; bk < 4; ++bk)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float r = fmaf(nbg[bk][v], XK[bk][v], vv[bk][v] * sv);
+                    XK[bk][v] = r;
+                    rmax = fmaxf(rmax, fabsf(r));
+                }
+        }
+        rmax = wave_max(rmax);
+        er = rescale_shift(rmax, -6, 8, 7, st.F);
+        if (er == 0) {
+            Br[0] = pack8(XK[0], XK[1]);
+            Br[1] = pack8(XK[2], XK[3]);
+        } else {
+            const float f = exp2i(-er);
+            Br[0] = pack8s(XK[0], XK[1], f);
+            Br[1] = pack8s(XK[2], XK[3], f);
+        }
+        // O^T starts as gamma_t (Q Stilde^T)^T in the scale of U.
+        const float fo = exp2i(-er);
+#pragma unroll
+        for (int tb2 = 0; tb2 < 4; ++tb2) OQ[tb2] *= gq[tb2] * fo;
+        RHZ_TRACE_POINT(c, 9);
+    }
+    RHZ_TRACE_POINT(c, 0);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 1);
+    // ---- interval B: U = T Rhat, O^T += U^T P^T, S update.
+    if (act) {
+        const int F1 = st.F + er;
+        // T rows (both 32-token halves for rows >= 32), P rows, decays.
+        f16x8 tr[6], pr[6];
+        f32x4 gd[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) tr[rb] = ld_f16x8(&sm.t[B][toff(tok(rb, n), 8 * g)]);
+#pragma unroll
+        for (int rb = 2; rb < 4; ++rb) tr[rb + 2] = ld_f16x8(&sm.t[B][toff(tok(rb, n), 32 + 8 * g)]);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            gd[2 * kk] = ld_f32x4(&sm.gdl[B][32 * kk + 8 * g]);
+            gd[2 * kk + 1] = ld_f32x4(&sm.gdl[B][32 * kk + 8 * g + 4]);
+        }
+        const float sd = sm.gam[B][63] * exp2i(-er);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 U[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = mfma16x32h(tr[rb], Br[0], acc);
+            if (rb >= 2) acc = mfma16x32h(tr[rb + 2], Br[1], acc);
+            U[rb] = acc;
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) pr[rb] = ld_f16x8(&sm.p[B][toff(16 * rb + n, 8 * g)]);
+#pragma unroll
+        for (int rb = 2; rb < 4; ++rb) pr[rb + 2] = ld_f16x8(&sm.p[B][toff(16 * rb + n, 32 + 8 * g)]);
+        f16x8 Bu[2], Bh[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            Bu[kk] = pack8(U[2 * kk], U[2 * kk + 1]);
+            Bh[kk] = pack8(U[2 * kk] * gd[2 * kk], U[2 * kk + 1] * gd[2 * kk + 1]);
+        }
+        RHZ_TRACE_POINT(c, 10);
+        // S update: K^T through transposed reads, 2 column blocks ahead.
+        s16x4 kt[NJ][4];
+        auto kt_load = [&](int jb) {
+            const int col = 32 * (jb >> 1) + 8 * (n & 3) + 4 * (jb & 1);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int row = 32 * kk + 8 * g + (n >> 2);
+                kt[jb][2 * kk] = ld_tr(&sm.k[B][KQ<DK>::off(row, col)]);
+                kt[jb][2 * kk + 1] = ld_tr(&sm.k[B][KQ<DK>::off(row + 4, col)]);
+            }
+        };
+        constexpr int kAhead = NJ < 2 ? NJ : 2;
+#pragma unroll
+        for (int jb = 0; jb < kAhead; ++jb) kt_load(jb);
+        // O^T[tb2] lane (n, g): token 16 tb2 + n, state rows orow + 0..3
+        f32x4 O[4];
+#pragma unroll
+        for (int tb2 = 0; tb2 < 4; ++tb2) {
+            f32x4 acc = mfma16x32h(Bu[0], pr[tb2], OQ[tb2]);
+            if (tb2 >= 2) acc = mfma16x32h(Bu[1], pr[tb2 + 2], acc);
+            O[tb2] = acc;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jb = 0; jb < NJ; ++jb) {
+            if (jb + kAhead < NJ) kt_load(jb + kAhead);
+            f32x4 acc = st.S[jb] * sd;
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const f16x8 ka = __builtin_bit_cast(
+                    f16x8, __builtin_shufflevector(kt[jb][2 * kk], kt[jb][2 * kk + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+                acc = mfma16x32h(ka, Bh[kk], acc);
+            }
+            st.S[jb] = acc;
+        }
+        // Output: 4 consecutive bf16 of one token per lane and block.
+        char* const obase = reinterpret_cast<char*>(p.o + (size_t(t0) * H + u.h) * dv);
+        const uint32_t ooff = (uint32_t(n) * H * dv + orow) * 2u;
+        const uint32_t tstride = 16u * H * dv * 2u;
+        if (F1 != 0) {
+            const float fout = exp2i(F1);
+#pragma unroll
+            for (int tb2 = 0; tb2 < 4; ++tb2) O[tb2] *= fout;
+        }
+#pragma unroll
+        for (int tb2 = 0; tb2 < 4; ++tb2)
+            if (16 * tb2 + n < len && orow < dv)
+                *reinterpret_cast<uint2*>(obase + ooff + tb2 * tstride) = pack_bf16x4(O[tb2]);
+        RHZ_TRACE_POINT(c, 11);
+        st.F = F1;
+        st.smax = state_max(st);
+        RHZ_TRACE_POINT(c, 12);
+    }
+    RHZ_TRACE_POINT(c, 2);
+    __syncthreads();
+    RHZ_TRACE_POINT(c, 3);
 }
 
 // ------------------------------------------------------------ fused kernel
 template <int DK>
 __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
-    constexpr int LDK = Smem<DK>::LDK;
-    constexpr int NK = DK / 32;  // 32-wide contraction steps over d_k
-    constexpr int NJ = DK / 16;  // 16-row blocks of key columns
+    constexpr int NK = DK / 32;
     __shared__ __align__(16) Smem<DK> sm;
 
     const int H = p.heads;
     int unit, tile;
     map_block(blockIdx.x, p.batch * H, p.n_tiles, unit, tile);
-    const int seqi = unit / H, h = unit - seqi * H;
-    const int seq = p.order ? p.order[seqi] : seqi;
-    int tb, te;
-    seq_bounds(p.cu_seqlens, seq, p.seq_len, tb, te);
-    const int nch = (te - tb + kChunk - 1) / kChunk;
-    const int i0 = tile * kTV;
+    const int seqi = unit / H;
+    Unit u;
+    u.h = unit - seqi * H;
+    u.seq = p.order ? p.order[seqi] : seqi;
+    seq_bounds(p.cu_seqlens, u.seq, p.seq_len, u.tb, u.te);
+    u.nch = (u.te - u.tb + kChunk - 1) / kChunk;
+    u.i0 = tile * kTV;
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int dk = p.d_k, dv = p.d_v;
@@ -390,207 +968,61 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         base[it % (2 * 64 * kLDT / 8)] = make_uint4(0, 0, 0, 0);
     }
 
+    // The chunk loop runs c = -1 .. nch-1 (c = -1 only prepares chunk 0),
+    // unrolled by two so that buffer c & 1 is a compile-time constant.
     if (w < 2) {
-        // ------------------------------------------------------ scan waves
         const int n = l & 15, g = l >> 4;
-        const int il = 16 * w + n, i = i0 + il;
-        const long srow = (((long)seq * H + h) * dv + i) * dk;
-        // S[jb][v] = S[i][tok(jb, 4g + v)]
-        f32x4 S[NJ];
+        const int i = u.i0 + 16 * w + n;
+        const size_t srow = ((size_t(u.seq) * H + u.h) * dv + i) * dk;
+        ScanState<DK> st;
 #pragma unroll
-        for (int jb = 0; jb < NJ; ++jb) S[jb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int jb = 0; jb < DK / 16; ++jb) st.S[jb] = (f32x4){0.f, 0.f, 0.f, 0.f};
         if (p.init && i < dv) {
 #pragma unroll
             for (int J = 0; J < NK; ++J) {
                 const int j = 32 * J + 8 * g;
                 if (j < dk) {
-                    const float4 a = *reinterpret_cast<const float4*>(p.init + srow + j);
-                    const float4 c = *reinterpret_cast<const float4*>(p.init + srow + j + 4);
-                    S[2 * J] = (f32x4){a.x, a.y, a.z, a.w};
-                    S[2 * J + 1] = (f32x4){c.x, c.y, c.z, c.w};
+                    st.S[2 * J] = ld_f32x4(p.init + srow + j);
+                    st.S[2 * J + 1] = ld_f32x4(p.init + srow + j + 4);
                 }
             }
         }
-        auto state_max = [&]() {
-            float m = 0.f;
-#pragma unroll
-            for (int jb = 0; jb < NJ; ++jb)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(S[jb][v]));
-            return wave_max(m);
-        };
-        float smax = state_max();
-
-        for (int c = -1; c < nch; ++c) {
-            const bool act = c >= 0;
-            const int b = c & 1;
-            const int t0 = tb + c * kChunk, len = min(kChunk, te - t0);
-            // ---- interval A: X = [K; Q] S0'^T, R, gamma X_Q.
-            f32x4 X[8];
-            f16x8 Br[2];
-            int eR = 0;
-            if (act) {
-                const int eS = smax > 0.f ? min(max(ilog2f(smax) - 14, -kMaxScaleExp), kMaxScaleExp) : 0;
-                f16x8 Bx[NK];
-#pragma unroll
-                for (int ks = 0; ks < NK; ++ks) Bx[ks] = pack8(S[2 * ks], S[2 * ks + 1], exp2i(-eS));
-#pragma unroll
-                for (int bk = 0; bk < 8; ++bk) {
-                    const uint16_t* src = bk < 4 ? sm.k[b] : sm.q[b];
-                    const int row = tok(bk & 3, n);
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(ld_f16x8(&src[row * LDK + 32 * ks + 8 * g]), Bx[ks], acc);
-                    X[bk] = acc;
-                }
-                const float up = exp2i(eS);
-                float rmax = 0.f;
-#pragma unroll
-                for (int bk = 0; bk < 4; ++bk) {
-                    const int s0 = 32 * (bk >> 1) + 8 * g + 4 * (bk & 1);
-                    const uint2 vv = *reinterpret_cast<const uint2*>(&sm.vt[b][il * kLDT + s0]);
-                    const float4 bs = *reinterpret_cast<const float4*>(&sm.bs[b][s0]);
-                    const float4 ga = *reinterpret_cast<const float4*>(&sm.gam[b][s0]);
-                    const float vf[4] = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
-                                         __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
-                    const float bv[4] = {bs.x, bs.y, bs.z, bs.w}, gv[4] = {ga.x, ga.y, ga.z, ga.w};
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const float r = bv[v] * (vf[v] - gv[v] * (X[bk][v] * up));
-                        X[bk][v] = r;
-                        rmax = fmaxf(rmax, fabsf(r));
-                    }
-                    const float4 gq = *reinterpret_cast<const float4*>(&sm.gam[b][s0]);
-                    X[4 + bk][0] *= gq.x * up;
-                    X[4 + bk][1] *= gq.y * up;
-                    X[4 + bk][2] *= gq.z * up;
-                    X[4 + bk][3] *= gq.w * up;
-                }
-                rmax = wave_max(rmax);
-                eR = rmax > 0.f ? min(max(ilog2f(rmax) - 7, -kMaxScaleExp), kMaxScaleExp) : 0;
-                const float sR = exp2i(-eR);
-                Br[0] = pack8(X[0], X[1], sR);
-                Br[1] = pack8(X[2], X[3], sR);
-            }
-            __syncthreads();
-            // ---- interval B: U' = T R', O = gamma X_Q + 2^eR P U', S update.
-            if (act) {
-                f32x4 U[4];
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    const int row = tok(rb, n);
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) acc = mfma16x32h(ld_f16x8(&sm.t[b][row * kLDT + 32 * kk + 8 * g]), Br[kk], acc);
-                    U[rb] = acc;
-                }
-                f16x8 Bu[2], Bh[2];
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    Bu[kk] = pack8(U[2 * kk], U[2 * kk + 1], 1.f);
-                    const float4 d0 = *reinterpret_cast<const float4*>(&sm.gdl[b][32 * kk + 8 * g]);
-                    const float4 d1 = *reinterpret_cast<const float4*>(&sm.gdl[b][32 * kk + 8 * g + 4]);
-                    f32x4 h0 = U[2 * kk], h1 = U[2 * kk + 1];
-                    h0[0] *= d0.x; h0[1] *= d0.y; h0[2] *= d0.z; h0[3] *= d0.w;
-                    h1[0] *= d1.x; h1[1] *= d1.y; h1[2] *= d1.z; h1[3] *= d1.w;
-                    Bh[kk] = pack8(h0, h1, 1.f);
-                }
-                const float down = exp2i(-eR), up = exp2i(eR);
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    const int row = tok(rb, n);
-                    f32x4 acc = X[4 + rb];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] *= down;
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) acc = mfma16x32h(ld_f16x8(&sm.p[b][row * kLDT + 32 * kk + 8 * g]), Bu[kk], acc);
-                    if (i < dv) {
-                        const int r0 = 32 * (rb >> 1) + 8 * g + 4 * (rb & 1);
-#pragma unroll
-                        for (int v = 0; v < 4; ++v)
-                            if (r0 + v < len) p.o[((long)(t0 + r0 + v) * H + h) * dv + i] = f32_to_bf16(acc[v] * up);
-                    }
-                }
-                const float sd = sm.gam[b][63] * down;
-#pragma unroll
-                for (int jb = 0; jb < NJ; ++jb) {
-                    f32x4 acc = S[jb];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] *= sd;
-                    const int col = 32 * (jb >> 1) + 8 * (n & 3) + 4 * (jb & 1);
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-                        const int row = 32 * kk + 8 * g + (n >> 2);
-                        const s16x4 lo = ld_tr(&sm.k[b][row * LDK + col]);
-                        const s16x4 hi = ld_tr(&sm.k[b][(row + 4) * LDK + col]);
-                        const f16x8 ka = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                        acc = mfma16x32h(ka, Bh[kk], acc);
-                    }
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] *= up;
-                    S[jb] = acc;
-                }
-                smax = state_max();
-            }
-            __syncthreads();
+        st.F = 0;
+        st.smax = state_max(st);
+        for (int c = -1; c < u.nch; c += 2) {
+            scan_chunk<DK, 1>(p, sm, u, c, w, l, st);
+            if (c + 1 < u.nch) scan_chunk<DK, 0>(p, sm, u, c + 1, w, l, st);
         }
         if (p.fin && i < dv) {
+            const float f = exp2i(st.F);
 #pragma unroll
             for (int J = 0; J < NK; ++J) {
                 const int j = 32 * J + 8 * g;
                 if (j < dk) {
-                    *reinterpret_cast<float4*>(p.fin + srow + j) =
-                        make_float4(S[2 * J][0], S[2 * J][1], S[2 * J][2], S[2 * J][3]);
-                    *reinterpret_cast<float4*>(p.fin + srow + j + 4) =
-                        make_float4(S[2 * J + 1][0], S[2 * J + 1][1], S[2 * J + 1][2], S[2 * J + 1][3]);
+                    const f32x4 a = st.S[2 * J] * f, c = st.S[2 * J + 1] * f;
+                    *reinterpret_cast<float4*>(p.fin + srow + j) = make_float4(a[0], a[1], a[2], a[3]);
+                    *reinterpret_cast<float4*>(p.fin + srow + j + 4) = make_float4(c[0], c[1], c[2], c[3]);
                 }
             }
         }
+    } else if (w == 2) {
+        for (int c = -1; c < u.nch; c += 2) {
+            prep_wave2<DK, 1>(sm, u, c, l);
+            if (c + 1 < u.nch) prep_wave2<DK, 0>(sm, u, c + 1, l);
+        }
+    } else if (w == 3) {
+        for (int c = -1; c < u.nch; c += 2) {
+            prep_wave3<DK, 1>(sm, u, c, l);
+            if (c + 1 < u.nch) prep_wave3<DK, 0>(sm, u, c + 1, l);
+        }
+    } else if (w == 4) {
+        loader_loop<DK, 0>(p, sm, u, tid - 256);
+    } else if (w == 5) {
+        loader_loop<DK, 1>(p, sm, u, tid - 256);
+    } else if (w == 6) {
+        loader_loop<DK, 2>(p, sm, u, tid - 256);
     } else {
-        // ------------------------------------------------------ prep waves
-        const bool loader = w >= 4;
-        const int lt = tid - 256;
-        ChunkIn<DK> in;
-        if (loader && nch > 0) load_chunk<DK>(p, h, tb, te, i0, 0, lt, in);
-        for (int c = -1; c < nch; ++c) {
-            const int nx = c + 1;  // chunk staged and prepared in this iteration
-            // ---- interval A: off-diagonal T blocks of chunk c (waves 2, 3);
-            //      stage chunk c+1, load chunk c+2 (waves 4-7).
-            if (loader) {
-                if (nx < nch) {
-                    stage_chunk<DK>(p, sm, tb, te, i0, nx, lt, in);
-                    load_chunk<DK>(p, h, tb, te, i0, min(nx + 1, nch - 1), lt, in);
-                }
-            } else if (c >= 0) {
-                uint16_t* tt = sm.t[c & 1];
-                if (w == 2) {
-                    t_block<DK>(sm, tt, 1, 0, l);
-                    lds_fence();
-                    t_block<DK>(sm, tt, 2, 0, l);
-                    lds_fence();
-                    t_block<DK>(sm, tt, 3, 0, l);
-                } else {
-                    t_block<DK>(sm, tt, 3, 2, l);
-                    t_block<DK>(sm, tt, 2, 1, l);
-                    lds_fence();
-                    t_block<DK>(sm, tt, 3, 1, l);
-                }
-            }
-            __syncthreads();
-            // ---- interval B: K K^T -> A and Q K^T -> P of chunk c+1 (waves
-            //      2, 3, 6, 7), then T's diagonal blocks (waves 2, 3).
-            if (nx < nch && (w == 2 || w == 3 || w == 6 || w == 7)) {
-                const int nb = nx & 1;
-                const bool isQ = w >= 6;
-                const int ra = (w & 1) ? 1 : 0, rb = (w & 1) ? 2 : 3;
-                kk_rows<DK>(sm, nb, isQ, ra, rb, l);
-                if (!isQ) {
-                    lds_fence();
-                    if (l < 32) t_diag<DK>(sm, sm.t[nb], l < 16 ? ra : rb, l & 15);
-                }
-            }
-            __syncthreads();
-        }
+        loader_loop<DK, 3>(p, sm, u, tid - 256);
     }
 }
 
