@@ -58,10 +58,6 @@
 #include "gdr_device.hpp"
 #include "gdr_internal.hpp"
 
-#ifndef RHZ_TRACE_POINT
-#define RHZ_TRACE_POINT(chunk, slot) ((void)0)
-#endif
-
 namespace rhz {
 namespace {
 
@@ -283,6 +279,50 @@ __device__ __forceinline__ void map_block(int bid, int units, int nt, int& unit,
     }
 }
 
+// ------------------------------------------------------------ wave sync
+// The waves of a workgroup synchronise through completion counters in LDS
+// instead of workgroup barriers, so that every wave waits only for the data
+// it consumes and the preparing waves run up to one chunk ahead of the scan.
+// Each counter counts (waves x chunks) finished; a wave that finishes a step
+// for chunk x adds 1 after its LDS writes have completed, and a consumer
+// waits until the counter reaches (number of producer waves) * (x + 1).  A
+// shared count is exact only because the producers of one counter cannot
+// drift apart by a chunk (each waits, before its next chunk, for a step that
+// needs all of them); the two scan waves can, so each has its own counter.
+// Every wait is for a step of an earlier or the same chunk of another role,
+// and each role processes its chunks in order, so the waits form an acyclic
+// graph; a wait also gives up after kSpinLimit polls, so the kernel ends even
+// if that property were ever broken.
+struct Sync {
+    int staged;  // loader waves (4 per chunk): K, Q, beta V, gates in LDS
+    int tdiag;   // wave 2 (1 per chunk): K K^T diagonal blocks and T's diagonal blocks
+    int aoff;    // wave 3 (1 per chunk): A below the diagonal
+    int tfull;   // waves 2, 3 (2 per chunk): T complete
+    int pdone;   // loader waves (4 per chunk): P
+    int scanned[2];  // scan wave w (1 per chunk): chunk finished, its buffers free
+};
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void signal(int* cnt) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are complete
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void wait_ge(int* cnt, int target);
+// Both scan waves have finished chunk x.
+__device__ __forceinline__ void wait_scanned(Sync& sy, int x) {
+    wait_ge(&sy.scanned[0], x + 1);
+    wait_ge(&sy.scanned[1], x + 1);
+}
+__device__ __forceinline__ void wait_ge(int* cnt, int target) {
+    for (int spin = 0; spin < kSpinLimit; ++spin) {
+        const int v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__builtin_amdgcn_readfirstlane(v) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+}
+
 // Shared memory of one workgroup.  Buffers indexed [2] are double-buffered
 // by chunk parity.  T and P hold zeros above the diagonal blocks for the
 // whole kernel.
@@ -303,6 +343,7 @@ struct Smem {
     float dst[2][64];                // exp(G_s - G_{16 floor(s/16)})
     float den[2][64];                // exp(G_{16 floor(s/16) + 15} - G_s)
     float pf[2][16];                 // [4 bi + bj]: exp(G_{16 bi} - G_{16 bj + 15}), bi > bj
+    Sync sync;
 };
 
 // Per-workgroup constants shared by the roles.
@@ -581,69 +622,59 @@ __device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
 }
 
 // ------------------------------------------------------------ prep roles
-// Wave 2, interval A: T_10, T_20, T_30 of chunk buffer B; interval B: K K^T
-// diagonal blocks and T's diagonal blocks of buffer 1 - B.
+// Wave 2, chunk x (buffer B = x & 1): K K^T's diagonal blocks and T's
+// diagonal blocks, then T_10, T_20, T_30.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, const Unit& u, int c, int l) {
-    constexpr int NB = 1 - B;
-    if (c >= 0) {
-        t_block<DK, B, 1, 0>(sm, l);
-        lds_fence();
-        t_block<DK, B, 2, 0>(sm, l);
-        lds_fence();
-        t_block<DK, B, 3, 0>(sm, l);
+__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l) {
+    constexpr int NK = DK / 32;
+    const int n = l & 15, g = l >> 4;
+    wait_ge(&sm.sync.staged, 4 * (x + 1));
+    if (x >= 2) {  // T[B] was read by the scan and written by both waves for chunk x - 2
+        wait_scanned(sm.sync, x - 2);
+        wait_ge(&sm.sync.tfull, 2 * (x - 1));
     }
-    RHZ_TRACE_POINT(c, 0);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 1);
-    if (c + 1 < u.nch) {
-        constexpr int NK = DK / 32;
-        const int n = l & 15, g = l >> 4;
-        f16x8 kr[4][NK];
+    f16x8 kr[4][NK];
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[NB], blk, n, g, kr[blk]);
-        kq_block<DK, NB, false, 0, 0>(sm, kr[0], kr[0], l);
-        kq_block<DK, NB, false, 1, 1>(sm, kr[1], kr[1], l);
-        kq_block<DK, NB, false, 2, 2>(sm, kr[2], kr[2], l);
-        kq_block<DK, NB, false, 3, 3>(sm, kr[3], kr[3], l);
-        lds_fence();
-        t_diag<DK, NB>(sm, l);
-    }
-    RHZ_TRACE_POINT(c, 2);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 3);
+    for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
+    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l);
+    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l);
+    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l);
+    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l);
+    lds_fence();
+    t_diag<DK, B>(sm, l);
+    signal(&sm.sync.tdiag);
+    wait_ge(&sm.sync.aoff, x + 1);
+    t_block<DK, B, 1, 0>(sm, l);
+    lds_fence();
+    t_block<DK, B, 2, 0>(sm, l);
+    lds_fence();
+    t_block<DK, B, 3, 0>(sm, l);
+    signal(&sm.sync.tfull);
 }
 
-// Wave 3, interval A: T_32, T_21, T_31 of buffer B; interval B: K K^T below
-// the diagonal of buffer 1 - B.
+// Wave 3, chunk x: K K^T below the diagonal into A, then T_32, T_21, T_31.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, const Unit& u, int c, int l) {
-    constexpr int NB = 1 - B;
-    if (c >= 0) {
-        t_block<DK, B, 3, 2>(sm, l);
-        t_block<DK, B, 2, 1>(sm, l);
-        lds_fence();
-        t_block<DK, B, 3, 1>(sm, l);
-    }
-    RHZ_TRACE_POINT(c, 0);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 1);
-    if (c + 1 < u.nch) {
-        constexpr int NK = DK / 32;
-        const int n = l & 15, g = l >> 4;
-        f16x8 kr[4][NK];
+__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l) {
+    constexpr int NK = DK / 32;
+    const int n = l & 15, g = l >> 4;
+    wait_ge(&sm.sync.staged, 4 * (x + 1));
+    wait_ge(&sm.sync.tfull, 2 * x);  // A (one buffer) was read by T's blocks of chunk x - 1
+    f16x8 kr[4][NK];
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[NB], blk, n, g, kr[blk]);
-        kq_block<DK, NB, false, 1, 0>(sm, kr[0], kr[1], l);
-        kq_block<DK, NB, false, 2, 0>(sm, kr[0], kr[2], l);
-        kq_block<DK, NB, false, 3, 0>(sm, kr[0], kr[3], l);
-        kq_block<DK, NB, false, 2, 1>(sm, kr[1], kr[2], l);
-        kq_block<DK, NB, false, 3, 1>(sm, kr[1], kr[3], l);
-        kq_block<DK, NB, false, 3, 2>(sm, kr[2], kr[3], l);
-    }
-    RHZ_TRACE_POINT(c, 2);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 3);
+    for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
+    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l);
+    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l);
+    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l);
+    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l);
+    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l);
+    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l);
+    signal(&sm.sync.aoff);
+    wait_ge(&sm.sync.tdiag, x + 1);
+    t_block<DK, B, 3, 2>(sm, l);
+    t_block<DK, B, 2, 1>(sm, l);
+    lds_fence();
+    t_block<DK, B, 3, 1>(sm, l);
+    signal(&sm.sync.tfull);
 }
 
 // Q K^T blocks of loader wave LW (0..3) for buffer NB:
@@ -684,25 +715,24 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
     }
 }
 
-// Loader waves 4-7, interval A: stage chunk c+1 into buffer 1 - B, load
-// chunk c+2; interval B: Q K^T of chunk c+1.
+// Loader wave LW, chunk x (buffer B = x & 1): stage x from registers, load
+// x + 1, then Q K^T of x.
 template <int DK, int B, int LW>
-__device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int c, int lt,
+__device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
-    constexpr int NB = 1 - B;
-    const int nx = c + 1;
-    if (nx < u.nch) {
-        const int len = min(kChunk, u.te - (u.tb + nx * kChunk));
-        stage_chunk<DK, NB, LW == kGateWave>(p, sm, len, u.i0, lt, in);
-        load_chunk_any<DK>(p, u, min(nx + 1, u.nch - 1), lo, lt, in);
+    if (x >= 2) {  // buffer B held chunk x - 2: every reader of it is done
+        wait_scanned(sm.sync, x - 2);
+        wait_ge(&sm.sync.pdone, 4 * (x - 1));
+        wait_ge(&sm.sync.tdiag, x - 1);
+        wait_ge(&sm.sync.aoff, x - 1);
     }
-    RHZ_TRACE_POINT(c, 0);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 1);
-    if (nx < u.nch) qk_blocks<DK, NB, LW>(sm, lt & 63);
-    RHZ_TRACE_POINT(c, 2);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 3);
+    const int len = min(kChunk, u.te - (u.tb + x * kChunk));
+    stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
+    signal(&sm.sync.staged);
+    if (x + 1 < u.nch) load_chunk_any<DK>(p, u, x + 1, lo, lt, in);
+    wait_ge(&sm.sync.staged, 4 * (x + 1));
+    qk_blocks<DK, B, LW>(sm, lt & 63);
+    signal(&sm.sync.pdone);
 }
 
 template <int DK, int LW>
@@ -711,9 +741,9 @@ __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, 
     lo.set(p, u.i0, lt, kChunk - 1);
     ChunkIn<DK> in;
     if (u.nch > 0) load_chunk_any<DK>(p, u, 0, lo, lt, in);
-    for (int c = -1; c < u.nch; c += 2) {
-        prep_loader<DK, 1, LW>(p, sm, u, c, lt, lo, in);
-        if (c + 1 < u.nch) prep_loader<DK, 0, LW>(p, sm, u, c + 1, lt, lo, in);
+    for (int x = 0; x < u.nch; x += 2) {
+        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, in);
+        if (x + 1 < u.nch) prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, in);
     }
 }
 
@@ -735,7 +765,7 @@ __device__ __forceinline__ float state_max(const ScanState<DK>& st) {
     return wave_max(m);
 }
 
-// One chunk of a scan wave (w = 0, 1) on buffer B.
+// Chunk c of a scan wave (w = 0, 1) on buffer B = c & 1.
 template <int DK, int B>
 __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int c, int w, int l,
                                            ScanState<DK>& st) {
@@ -745,13 +775,13 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
     const int il = 16 * w + n;
     const int orow = u.i0 + 16 * w + 4 * g;  // first of the 4 output rows of this lane
     const int H = p.heads, dv = p.d_v;
-    const bool act = c >= 0;
     const int t0 = u.tb + c * kChunk, len = min(kChunk, u.te - t0);
-    // ---- interval A: X_K = K Stilde^T -> Rtilde;  O^T <- (Q Stilde^T)^T.
+    // ---- X_K = K Stilde^T -> Rtilde;  O^T <- (Q Stilde^T)^T.
     f32x4 OQ[4];
     f16x8 Br[2];
     int er = 0;
-    if (act) {
+    wait_ge(&sm.sync.staged, 4 * (c + 1));
+    {
         // Operands of this interval, read ahead of their products.
         f16x8 kx[4][NK];
 #pragma unroll
@@ -807,7 +837,6 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
             for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(Bx[ks], qx[tb2][ks], acc);
             OQ[tb2] = acc;
         }
-        RHZ_TRACE_POINT(c, 8);
         float rmax = 0.f;
         if (st.F == 0) {
 #pragma unroll
@@ -843,13 +872,11 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         const float fo = exp2i(-er);
 #pragma unroll
         for (int tb2 = 0; tb2 < 4; ++tb2) OQ[tb2] *= gq[tb2] * fo;
-        RHZ_TRACE_POINT(c, 9);
     }
-    RHZ_TRACE_POINT(c, 0);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 1);
-    // ---- interval B: U = T Rhat, O^T += U^T P^T, S update.
-    if (act) {
+    // ---- U = T Rhat, O^T += U^T P^T, S update.
+    wait_ge(&sm.sync.tfull, 2 * (c + 1));
+    wait_ge(&sm.sync.pdone, 4 * (c + 1));
+    {
         const int F1 = st.F + er;
         // T rows (both 32-token halves for rows >= 32), P rows, decays.
         f16x8 tr[6], pr[6];
@@ -883,7 +910,6 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
             Bu[kk] = pack8(U[2 * kk], U[2 * kk + 1]);
             Bh[kk] = pack8(U[2 * kk] * gd[2 * kk], U[2 * kk + 1] * gd[2 * kk + 1]);
         }
-        RHZ_TRACE_POINT(c, 10);
         // S update: K^T through transposed reads, 2 column blocks ahead.
         s16x4 kt[NJ][4];
         auto kt_load = [&](int jb) {
@@ -932,14 +958,10 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         for (int tb2 = 0; tb2 < 4; ++tb2)
             if (16 * tb2 + n < len && orow < dv)
                 *reinterpret_cast<uint2*>(obase + ooff + tb2 * tstride) = pack_bf16x4(O[tb2]);
-        RHZ_TRACE_POINT(c, 11);
         st.F = F1;
         st.smax = state_max(st);
-        RHZ_TRACE_POINT(c, 12);
     }
-    RHZ_TRACE_POINT(c, 2);
-    __syncthreads();
-    RHZ_TRACE_POINT(c, 3);
+    signal(&sm.sync.scanned[w]);
 }
 
 // ------------------------------------------------------------ fused kernel
@@ -967,9 +989,11 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         uint4* base = reinterpret_cast<uint4*>(it < 2 * 64 * kLDT / 8 ? &sm.t[0][0] : &sm.p[0][0]);
         base[it % (2 * 64 * kLDT / 8)] = make_uint4(0, 0, 0, 0);
     }
+    if (tid == 0) sm.sync = Sync{0, 0, 0, 0, 0, {0, 0}};
+    __syncthreads();  // the only workgroup barrier: the chunk loops sync through sm.sync
 
-    // The chunk loop runs c = -1 .. nch-1 (c = -1 only prepares chunk 0),
-    // unrolled by two so that buffer c & 1 is a compile-time constant.
+    // Every role runs chunks 0 .. nch-1, unrolled by two so that buffer c & 1
+    // is a compile-time constant.
     if (w < 2) {
         const int n = l & 15, g = l >> 4;
         const int i = u.i0 + 16 * w + n;
@@ -989,9 +1013,9 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         }
         st.F = 0;
         st.smax = state_max(st);
-        for (int c = -1; c < u.nch; c += 2) {
-            scan_chunk<DK, 1>(p, sm, u, c, w, l, st);
-            if (c + 1 < u.nch) scan_chunk<DK, 0>(p, sm, u, c + 1, w, l, st);
+        for (int c = 0; c < u.nch; c += 2) {
+            scan_chunk<DK, 0>(p, sm, u, c, w, l, st);
+            if (c + 1 < u.nch) scan_chunk<DK, 1>(p, sm, u, c + 1, w, l, st);
         }
         if (p.fin && i < dv) {
             const float f = exp2i(st.F);
@@ -1006,14 +1030,14 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
             }
         }
     } else if (w == 2) {
-        for (int c = -1; c < u.nch; c += 2) {
-            prep_wave2<DK, 1>(sm, u, c, l);
-            if (c + 1 < u.nch) prep_wave2<DK, 0>(sm, u, c + 1, l);
+        for (int x = 0; x < u.nch; x += 2) {
+            prep_wave2<DK, 0>(sm, x, l);
+            if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l);
         }
     } else if (w == 3) {
-        for (int c = -1; c < u.nch; c += 2) {
-            prep_wave3<DK, 1>(sm, u, c, l);
-            if (c + 1 < u.nch) prep_wave3<DK, 0>(sm, u, c + 1, l);
+        for (int x = 0; x < u.nch; x += 2) {
+            prep_wave3<DK, 0>(sm, x, l);
+            if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l);
         }
     } else if (w == 4) {
         loader_loop<DK, 0>(p, sm, u, tid - 256);
