@@ -557,18 +557,30 @@ __device__ __forceinline__ float bcast_fma(float a, float t, float acc) {
     asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(a), "v"(t), "i"(R));
     return acc;
 }
-// Row R of the forward substitution: t_R = -sum_{s<R} A[R][s] t_s, A[R][s]
-// broadcast from the lane that holds row R.
+// Forward substitution t_R = -sum_{s<R} A[R][s] t_s in column order: once t_S
+// is final it is folded into the partial sums of every later row R > S, with
+// A[R][S] broadcast from the lane that holds row R.  Each row still sums its
+// terms in increasing s, but the rows' sums advance together, so the
+// dependent chain is one multiply-add per row instead of one per term.
 template <int R>
-__device__ __forceinline__ void t_diag_row(float* t, const float* a, int col) {
-    float acc = bcast_mul<R>(a[0], t[0]);
-#pragma unroll
-    for (int s = 1; s < R; ++s) acc = bcast_fma<R>(a[s], t[s], acc);
-    if (R > col) t[R] = -acc;
+__device__ __forceinline__ void t_diag_init(float* acc, const float* a, const float* t) {
+    acc[R] = bcast_mul<R>(a[0], t[0]);
 }
-template <int... R>
-__device__ __forceinline__ void t_diag_rows(float* t, const float* a, int col, std::integer_sequence<int, R...>) {
-    (t_diag_row<R + 1>(t, a, col), ...);
+template <int S, int R>
+__device__ __forceinline__ void t_diag_fold(float* acc, const float* a, const float* t) {
+    acc[R] = bcast_fma<R>(a[S], t[S], acc[R]);
+}
+template <int S, int... R>
+__device__ __forceinline__ void t_diag_col(float* t, float* acc, const float* a, int col,
+                                           std::integer_sequence<int, R...>) {
+    if (S > col) t[S] = -acc[S];
+    (t_diag_fold<S, S + 1 + R>(acc, a, t), ...);
+}
+template <int... S>
+__device__ __forceinline__ void t_diag_solve(float* t, const float* a, int col, std::integer_sequence<int, S...>) {
+    float acc[16];
+    (t_diag_init<S + 1>(acc, a, t), ...);
+    (t_diag_col<S + 1>(t, acc, a, col, std::make_integer_sequence<int, 14 - S>{}), ...);
 }
 
 // Diagonal blocks of T = (I + A)^-1 by forward substitution in fp32, one
@@ -587,7 +599,7 @@ __device__ __forceinline__ void t_diag(Smem<DK>& sm, int l) {
     float t[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) t[r] = r == col ? 1.f : 0.f;
-    t_diag_rows(t, a, col, std::make_integer_sequence<int, 15>{});
+    t_diag_solve(t, a, col, std::make_integer_sequence<int, 15>{});
 #pragma unroll
     for (int r = 0; r < 16; ++r) sm.t[NB][toff(16 * blk + r, 16 * blk + col)] = f32_to_f16(t[r]);
 }
