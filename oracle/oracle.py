@@ -91,11 +91,15 @@ def _pn(a):
     return None if a is None else _p(a)
 
 
+MAX_THREADS = 16  # the host CPU share one GPU is given
+
+
 def default_threads() -> int:
     try:
-        return max(1, len(os.sched_getaffinity(0)))
+        n = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        return os.cpu_count() or 1
+        n = os.cpu_count() or 1
+    return max(1, min(n, MAX_THREADS))
 
 
 # ----------------------------------------------------------------- Philox
