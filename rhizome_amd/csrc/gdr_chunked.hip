@@ -28,19 +28,22 @@
 // ds_read_b64_tr_b16, and O is produced transposed, so that each lane stores
 // 4 consecutive outputs of one token.
 //
-// The other six waves prepare the state-independent data one chunk ahead,
-// in lockstep with two barriers per chunk:
-//   interval A: scan X, R  |  T's off-diagonal 16x16 blocks of chunk c
-//               (waves 2, 3)  |  K, Q, beta V and the gates of chunk c+1 into
-//               LDS from registers, and chunk c+2 into registers (waves 4-7);
-//   interval B: scan U, O, S update  |  for chunk c+1: K K^T's diagonal
-//               blocks and T's diagonal blocks by forward substitution
-//               (wave 2), K K^T below the diagonal (wave 3), Q K^T (waves
-//               4-7).
+// The other six waves prepare the state-independent data of the next chunk
+// into the other half of double-buffered LDS:
+//   waves 4-7 (loaders): K, Q, beta V and the gates of chunk c into LDS from
+//               registers, chunk c+1 into registers, then Q K^T of chunk c;
+//   wave 2:     K K^T's diagonal blocks, T's diagonal blocks by forward
+//               substitution, T's blocks (1,0), (2,0), (3,0);
+//   wave 3:     K K^T below the diagonal, T's blocks (3,2), (2,1), (3,1).
 // T = (I + A)^-1 is blocked forward substitution: diagonal blocks by
-// substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.  The chunk loop
-// is unrolled by two, so that the double-buffer index is a compile-time
-// constant and every LDS address is a per-lane base plus an immediate.
+// substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.  There is no
+// workgroup barrier in the chunk loop: each role publishes its progress in
+// an LDS counter (incremented by one lane after the wave's LDS writes have
+// completed) and waits, by polling, for the counters it depends on; a
+// buffer is refilled only after both scan waves have counted the chunk that
+// last used it.  The chunk loop is unrolled by two, so that the
+// double-buffer index is a compile-time constant and every LDS address is a
+// per-lane base plus an immediate.
 //
 // Operand precision: every GEMM runs on fp16 MFMA (11-bit significands)
 // with fp32 accumulation; the carried state is fp32.  K and Q are the bf16
