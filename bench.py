@@ -6,7 +6,8 @@ B=4, H=16, T=4096, d_k=d_v=128, bf16 q/k/v, fp32 gates/state, chunk 64 --
 one step = one rhz_gdr_prefill over the whole batch (all heads), inputs
 resident in HBM.  Alongside (`decode`): the decode state update on B=256,
 H=16, d=128, fp32 state, one rhz_gdr_decode_step launch per step over 64
-steps, as HBM GB/s.
+steps, as HBM GB/s; and (`multistep`) rhz_gdr_multistep over 8 positions on
+the same shape, as HBM GB/s.
 
 Inputs are synthetic and seeded: the reference's Philox-4x32-10 streams
 (q=1, k=2, v=3, beta=4, g=5, state=6), generated on the device by
@@ -45,6 +46,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 PREFILL = dict(batch=4, heads=16, seq_len=4096, d_k=128, d_v=128, chunk=64)
 DECODE = dict(batch=256, heads=16, d_k=128, d_v=128, steps=64)
+MULTISTEP = dict(batch=256, heads=16, d_k=128, d_v=128, positions=8)
 
 
 def prefill_flops(lengths, heads, dk, dv, chunk=64) -> float:
@@ -84,6 +86,11 @@ def traffic_from_profiles(kind: str):
         if m:
             return float(m.group(1))
     return None
+
+
+def multistep_bytes(batch, heads, dk, dv, n) -> float:
+    """fp32 state read once, n snapshots written, n positions of fp32 q, k, v, o and gates."""
+    return float(batch * heads * (4 * dk * dv * (1 + n) + n * (4 * (2 * dk + 2 * dv) + 8)))
 
 
 def time_region(torch, stream, fn, reps: int) -> float:
@@ -166,6 +173,36 @@ def bench_decode(torch, warmup):
         step()
     ms = time_region(torch, stream, step, n)
     return ms, decode_bytes(B, H, dk, dv), {"q": q, "k": k, "v": v, "g": g, "beta": beta}
+
+
+def bench_multistep(torch, steps, warmup):
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = MULTISTEP
+    B, H, dk, dv, n = c["batch"], c["heads"], c["d_k"], c["d_v"], c["positions"]
+    f32 = torch.float32
+    q = rhizome_amd.philox_fill("unit_rows", 0, 1, (B, n, H, dk), f32)
+    k = rhizome_amd.philox_fill("unit_rows", 0, 2, (B, n, H, dk), f32)
+    v = rhizome_amd.philox_fill("normal", 0, 3, (B, n, H, dv), f32)
+    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, (B, n, H), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, (B, n, H), f32)
+    state = rhizome_amd.philox_fill("normal", 0, 6, (B, H, dv, dk), f32, std=0.02)
+    o = torch.empty((B, n, H, dv), dtype=f32, device=q.device)
+    states = torch.empty((B, n, H, dv, dk), dtype=f32, device=q.device)
+    args = gdr.multistep_args(q, k, v, g, beta, _abi.GATE_LOG_ALPHA, state, states, o)
+    stream = torch.cuda.current_stream()
+    lib, argp, sp = _abi.lib(), ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream or None)
+
+    def step():
+        st = lib.rhz_gdr_multistep(argp, sp)
+        if st:
+            _abi.check(st)
+
+    for _ in range(warmup):
+        step()
+    ms = time_region(torch, stream, step, steps)
+    return ms, multistep_bytes(B, H, dk, dv, n)
 
 
 def cpu_baseline(pre_host, dec_host):
@@ -264,6 +301,7 @@ def main() -> int:
         return 1
     ms, flops, algo_bytes, pre_host = bench_prefill(torch, args.steps, args.warmup)
     dms, dbytes, dec_host = bench_decode(torch, args.warmup)
+    mms, mbytes = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
     if args.calibration_copy:
         calibration_copy(torch)
     c = PREFILL
@@ -308,6 +346,15 @@ def main() -> int:
                                 "traffic": traffic_from_profiles("decode"),
                                 "kernel": "gdr_decode_kernel<8,4,true,float>",
                                 "bytes_per_launch": dbytes, "launch_us": dms * 1e3}},
+        "multistep": {"metric": "multistep HBM GB/s (state read, per-position snapshots written)",
+                      "value": mbytes / (mms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": mms,
+                      "config": {"workload": "GDR multistep, 8 positions from a given state",
+                                 **MULTISTEP, "dtype": "fp32"},
+                      "roofline": {"bound": "hbm", "achieved": mbytes / (mms * 1e-3) / 1e9,
+                                   "peak": PEAK_HBM_GBS,
+                                   "frac": mbytes / (mms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                   "kernel": "gdr_multistep_kernel<8,4,true,float>",
+                                   "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu_baseline:

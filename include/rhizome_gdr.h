@@ -68,8 +68,9 @@ typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUN
 /* Op identities for rhz_gdr_query_support, named after the plan-level ops
  * OpKind::DeltaScan / OpKind::DeltaStep (crates/plan/src/graph.rs:56-59). */
 typedef enum rhz_op {
-    RHZ_OP_DELTA_SCAN = 0, /* "gated_delta_scan_chunked" (graph.rs:124) */
-    RHZ_OP_DELTA_STEP = 1  /* "gated_delta_step" (graph.rs:125) */
+    RHZ_OP_DELTA_SCAN = 0,     /* "gated_delta_scan_chunked" (graph.rs:124) */
+    RHZ_OP_DELTA_STEP = 1,     /* "gated_delta_step" (graph.rs:125) */
+    RHZ_OP_DELTA_MULTISTEP = 2 /* gated_delta_multistep (delta.rs:202-230); no plan-level op */
 } rhz_op;
 
 /* Prefill over a dense batch or a packed variable-length batch.
@@ -122,6 +123,34 @@ typedef struct rhz_gdr_decode_args {
     void* o;           /* [B, H, d_v] */
 } rhz_gdr_decode_args;
 
+/* Up to `steps` consecutive positions for every (b, h) from a given state,
+ * returning o and the state after every position (speculative decoding:
+ * the snapshot of the last accepted position becomes the new state).
+ * Replaces gated_delta_multistep (delta.rs:202-230), batched.  Unlike it,
+ * the given state is honoured (the reference resets S at t = 0: pass zeros
+ * for its behaviour); a segment change inside the window is a gate of
+ * alpha = 0 at that position (RHZ_GATE_ALPHA), which forgets the past
+ * exactly as the reference's reset does.  `state` is read only. */
+typedef struct rhz_gdr_multistep_args {
+    int32_t batch;     /* B >= 1 */
+    int32_t steps;     /* positions n, 1..RHZ_MULTISTEP_MAX */
+    int32_t heads;     /* H >= 1 */
+    int32_t d_k;       /* 1..256 */
+    int32_t d_v;       /* 1..1024 */
+    int32_t dtype;     /* rhz_dtype of q, k, v and o */
+    int32_t gate_kind; /* rhz_gate */
+    const void* q;      /* [B, n, H, d_k] */
+    const void* k;      /* [B, n, H, d_k] */
+    const void* v;      /* [B, n, H, d_v] */
+    const float* gate;  /* [B, n, H] */
+    const float* beta;  /* [B, n, H] */
+    const float* state; /* [B, H, d_v, d_k] fp32, the state before position 0 */
+    float* states;      /* [B, n, H, d_v, d_k] fp32 out: the state after each position */
+    void* o;            /* [B, n, H, d_v] */
+} rhz_gdr_multistep_args;
+
+#define RHZ_MULTISTEP_MAX 64
+
 /* Library identity. */
 int32_t rhz_gdr_abi_version(void);
 
@@ -147,6 +176,9 @@ rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream);
 
 /* Gated delta-rule decode step (see rhz_gdr_decode_args). */
 rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* args, void* stream);
+
+/* Gated delta-rule multistep (see rhz_gdr_multistep_args). */
+rhz_status rhz_gdr_multistep(const rhz_gdr_multistep_args* args, void* stream);
 
 /* Seeded synthetic inputs on the device, from the reference's Philox-4x32-10
  * (crates/ops/src/rng.rs:43-90; elementwise.rs:5-12, 36-42, 125-128).

@@ -5,6 +5,6 @@ The compute lives in librhizome_gdr.so (hand-written HIP kernels, built by
 end.  Importing the package does not load the library; the first call does,
 and raises if the library is missing.
 """
-from .gdr import decode_step, philox_fill, prefill, query_support  # noqa: F401
+from .gdr import decode_step, multistep, philox_fill, prefill, query_support  # noqa: F401
 
-__all__ = ["prefill", "decode_step", "philox_fill", "query_support"]
+__all__ = ["prefill", "decode_step", "multistep", "philox_fill", "query_support"]

@@ -25,7 +25,8 @@ GATE_LOG_ALPHA, GATE_ALPHA = 0, 1
 # rhz_algo
 ALGO_AUTO, ALGO_RECURRENT, ALGO_CHUNKED = 0, 1, 2
 # rhz_op
-OP_DELTA_SCAN, OP_DELTA_STEP = 0, 1
+OP_DELTA_SCAN, OP_DELTA_STEP, OP_DELTA_MULTISTEP = 0, 1, 2
+MULTISTEP_MAX = 64
 # rhz_fill_kind
 FILL_NORMAL, FILL_UNIT_ROWS, FILL_SIGMOID, FILL_NEG_SOFTPLUS = 0, 1, 2, 3
 
@@ -47,6 +48,15 @@ class DecodeArgs(Structure):
         ("dtype", c_int32), ("gate_kind", c_int32),
         ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("gate", c_void_p), ("beta", c_void_p),
         ("state", c_void_p), ("o", c_void_p),
+    ]
+
+
+class MultistepArgs(Structure):
+    _fields_ = [
+        ("batch", c_int32), ("steps", c_int32), ("heads", c_int32), ("d_k", c_int32),
+        ("d_v", c_int32), ("dtype", c_int32), ("gate_kind", c_int32),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("gate", c_void_p), ("beta", c_void_p),
+        ("state", c_void_p), ("states", c_void_p), ("o", c_void_p),
     ]
 
 
@@ -88,6 +98,8 @@ def lib():
         L.rhz_gdr_prefill.restype = c_int32
         L.rhz_gdr_decode_step.argtypes = [POINTER(DecodeArgs), c_void_p]
         L.rhz_gdr_decode_step.restype = c_int32
+        L.rhz_gdr_multistep.argtypes = [POINTER(MultistepArgs), c_void_p]
+        L.rhz_gdr_multistep.restype = c_int32
         L.rhz_philox_fill.argtypes = [c_int32, c_uint64, c_uint64, c_int64, c_int32, c_double,
                                       c_double, c_int32, c_void_p, c_void_p]
         L.rhz_philox_fill.restype = c_int32

@@ -134,14 +134,16 @@ const char* rhz_status_string(int32_t status) {
 const char* rhz_last_error(void) { return g_last_error.c_str(); }
 
 rhz_status rhz_gdr_query_support(int32_t op, int32_t dtype, int32_t d_k, int32_t d_v, int32_t algo) {
-    if (op != RHZ_OP_DELTA_SCAN && op != RHZ_OP_DELTA_STEP) return fail(RHZ_ERR_INVALID_ARG, "unknown op %d", op);
+    if (op != RHZ_OP_DELTA_SCAN && op != RHZ_OP_DELTA_STEP && op != RHZ_OP_DELTA_MULTISTEP)
+        return fail(RHZ_ERR_INVALID_ARG, "unknown op %d", op);
     if (dtype != RHZ_F32 && dtype != RHZ_BF16) return fail(RHZ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
     if (algo < RHZ_ALGO_AUTO || algo > RHZ_ALGO_CHUNKED) return fail(RHZ_ERR_INVALID_ARG, "unknown algo %d", algo);
     if (d_k < 1 || d_v < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k and d_v must be >= 1");
     if (d_k > 256 || d_v > 1024)
         return fail(RHZ_ERR_UNSUPPORTED, "d_k <= 256 and d_v <= 1024 are supported (got %d, %d)", d_k, d_v);
-    if (op == RHZ_OP_DELTA_STEP) {
-        if (algo == RHZ_ALGO_CHUNKED) return fail(RHZ_ERR_UNSUPPORTED, "the decode step has no CHUNKED algorithm");
+    if (op == RHZ_OP_DELTA_STEP || op == RHZ_OP_DELTA_MULTISTEP) {
+        if (algo == RHZ_ALGO_CHUNKED)
+            return fail(RHZ_ERR_UNSUPPORTED, "the decode step and multistep have no CHUNKED algorithm");
         return ok();
     }
     if (algo == RHZ_ALGO_CHUNKED) {
@@ -211,6 +213,44 @@ rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* a, void* stream) {
         reinterpret_cast<uintptr_t>(a->state) % 4)
         return fail(RHZ_ERR_INVALID_ARG, "fp32 tensors must be 4-byte aligned");
     return hip_status(rhz::launch_decode(*a, static_cast<hipStream_t>(stream)), "decode step launch");
+}
+
+rhz_status rhz_gdr_multistep(const rhz_gdr_multistep_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->batch < 1) return fail(RHZ_ERR_INVALID_ARG, "batch must be >= 1 (got %d)", a->batch);
+    if (a->steps < 1) return fail(RHZ_ERR_INVALID_ARG, "steps must be >= 1 (got %d)", a->steps);
+    if (a->heads < 1) return fail(RHZ_ERR_INVALID_ARG, "heads must be >= 1 (got %d)", a->heads);
+    if (a->d_k < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k must be >= 1 (got %d)", a->d_k);
+    if (a->d_v < 1) return fail(RHZ_ERR_INVALID_ARG, "d_v must be >= 1 (got %d)", a->d_v);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (a->gate_kind != RHZ_GATE_LOG_ALPHA && a->gate_kind != RHZ_GATE_ALPHA)
+        return fail(RHZ_ERR_INVALID_ARG, "gate_kind must be RHZ_GATE_LOG_ALPHA or RHZ_GATE_ALPHA (got %d)",
+                    a->gate_kind);
+    if (a->steps > RHZ_MULTISTEP_MAX)
+        return fail(RHZ_ERR_UNSUPPORTED, "steps = %d exceeds the supported %d", a->steps, RHZ_MULTISTEP_MAX);
+    if (a->d_k > 256) return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d exceeds the supported 256", a->d_k);
+    if (a->d_v > 1024) return fail(RHZ_ERR_UNSUPPORTED, "d_v = %d exceeds the supported 1024", a->d_v);
+    if ((int64_t)a->batch * a->heads * a->steps > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "batch * steps * heads exceeds 2^31 - 1");
+    if (!a->q) return fail(RHZ_ERR_INVALID_ARG, "q is NULL");
+    if (!a->k) return fail(RHZ_ERR_INVALID_ARG, "k is NULL");
+    if (!a->v) return fail(RHZ_ERR_INVALID_ARG, "v is NULL");
+    if (!a->gate) return fail(RHZ_ERR_INVALID_ARG, "gate is NULL");
+    if (!a->beta) return fail(RHZ_ERR_INVALID_ARG, "beta is NULL");
+    if (!a->state) return fail(RHZ_ERR_INVALID_ARG, "state is NULL");
+    if (!a->states) return fail(RHZ_ERR_INVALID_ARG, "states is NULL");
+    if (!a->o) return fail(RHZ_ERR_INVALID_ARG, "o is NULL");
+    const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+    const void* ptrs[] = {a->q, a->k, a->v, a->o};
+    const char* names[] = {"q", "k", "v", "o"};
+    for (int i = 0; i < 4; ++i)
+        if (reinterpret_cast<uintptr_t>(ptrs[i]) % ea)
+            return fail(RHZ_ERR_INVALID_ARG, "%s is not aligned to its element size", names[i]);
+    if (reinterpret_cast<uintptr_t>(a->gate) % 4 || reinterpret_cast<uintptr_t>(a->beta) % 4 ||
+        reinterpret_cast<uintptr_t>(a->state) % 4 || reinterpret_cast<uintptr_t>(a->states) % 4)
+        return fail(RHZ_ERR_INVALID_ARG, "fp32 tensors must be 4-byte aligned");
+    return hip_status(rhz::launch_multistep(*a, static_cast<hipStream_t>(stream)), "multistep launch");
 }
 
 rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count, int32_t row_len,

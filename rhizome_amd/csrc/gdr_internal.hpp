@@ -17,6 +17,10 @@ hipError_t launch_recurrent(const rhz_gdr_prefill_args& a, hipStream_t stream);
 // One decode position for every (b, h), state in place.
 hipError_t launch_decode(const rhz_gdr_decode_args& a, hipStream_t stream);
 
+// Up to RHZ_MULTISTEP_MAX positions for every (b, h), with per-position
+// state snapshots.
+hipError_t launch_multistep(const rhz_gdr_multistep_args& a, hipStream_t stream);
+
 // Chunked WY/UT prefill (bf16 in, fp32 state).  Requires d_k % 8 == 0,
 // d_k <= 128, d_v % 8 == 0 and 16-byte aligned tensors.
 bool chunked_supported(int d_k, int d_v);

@@ -3,6 +3,10 @@
 //   gdr_decode_kernel     one position for every (b, h), state streamed from
 //                         HBM and written back in place (gated_delta_step,
 //                         crates/ops/src/delta.rs:94-127, batched);
+//   gdr_multistep_kernel  up to a few positions for every (b, h) with the
+//                         state rows in registers, writing o and the state
+//                         after every position (gated_delta_multistep,
+//                         delta.rs:202-230, batched, without its t = 0 reset);
 //   gdr_recurrent_kernel  the same update carried token by token through a
 //                         whole sequence with the state rows in registers
 //                         (gated_delta_sequential, delta.rs:133-154, without
@@ -34,6 +38,18 @@ struct StepParams {
     float* state;
     void* o;
     int d_k, d_v, gate_is_alpha;
+};
+
+struct MultiParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* gate;
+    const float* beta;
+    const float* state;
+    float* states;
+    void* o;
+    int steps, heads, d_k, d_v, gate_is_alpha;
 };
 
 struct SeqParams {
@@ -161,6 +177,84 @@ __global__ __launch_bounds__(256) void gdr_decode_kernel(StepParams p) {
     }
 }
 
+// ------------------------------------------------------------- multistep
+// Grid: x = b*H + h, y = block of P*RPP rows, as the decode kernel; the rows
+// stay in registers across the n positions, and each position's k, q, v and
+// gates are loaded while the previous one is applied.
+template <int LPR, int P, bool VEC, typename T>
+__global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
+    constexpr int RPP = 256 / LPR;
+    const int bh = blockIdx.x;
+    const int b = bh / p.heads, h = bh - b * p.heads;
+    const int li = threadIdx.x % LPR;
+    const int rl = threadIdx.x / LPR;
+    const int dk = p.d_k, dv = p.d_v, H = p.heads, n = p.steps;
+    const int rbase = blockIdx.y * (P * RPP) + rl;
+    const float* S0 = p.state + (long)bh * dv * dk;
+
+    float s[P][16];
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+        const int r = rbase + pp * RPP;
+        if (r < dv) {
+            load_slice<LPR, VEC, float>(S0 + (long)r * dk, li, dk, s[pp]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[pp][e] = 0.f;
+        }
+    }
+    const T* qp = static_cast<const T*>(p.q);
+    const T* kp = static_cast<const T*>(p.k);
+    const T* vp = static_cast<const T*>(p.v);
+    T* op = static_cast<T*>(p.o);
+
+    // position t of (b, h): row (b n + t) H + h of every [B, n, H, ...] tensor
+    float kn[16], qn[16], vn[P], gn = 0.f, bn = 0.f;
+    auto fetch = [&](int t) {
+        const long th = ((long)b * n + t) * H + h;
+        load_slice<LPR, VEC, T>(kp + th * dk, li, dk, kn);
+        load_slice<LPR, VEC, T>(qp + th * dk, li, dk, qn);
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            const int r = rbase + pp * RPP;
+            vn[pp] = r < dv ? Elem<T>::load(vp, th * dv + r) : 0.f;
+        }
+        gn = p.gate[th];
+        bn = p.beta[th];
+    };
+    fetch(0);
+    for (int t = 0; t < n; ++t) {
+        float kr[16], qr[16], vr[P];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            kr[e] = kn[e];
+            qr[e] = qn[e];
+        }
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) vr[pp] = vn[pp];
+        const float ga = gn, be = bn;
+        if (t + 1 < n) fetch(t + 1);
+        const float alpha = decay_factor(ga, p.gate_is_alpha);
+        const float kq = group_sum<LPR>(dot16(kr, qr));
+        const long th = ((long)b * n + t) * H + h;
+        float* snap = p.states + th * dv * dk;
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            const int r = rbase + pp * RPP;
+            const float sk = group_sum<LPR>(dot16(s[pp], kr));
+            const float sq = group_sum<LPR>(dot16(s[pp], qr));
+            const float c = be * (vr[pp] - alpha * sk);
+            const float oi = alpha * sq + c * kq;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
+            if (r < dv) {
+                store_slice<LPR, VEC>(snap + (long)r * dk, li, dk, s[pp]);
+                if (li == 0) Elem<T>::store(op, th * dv + r, oi);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------- recurrent prefill
 // Grid: x = seq*H + h, y = block of RPW = 64/LPR rows; one wave per block.
 // The next token's k, q, v and gates are loaded while the current one is
@@ -252,6 +346,33 @@ hipError_t decode_pick_lpr(const StepParams& sp, int units, int dk, int dv, hipS
     }
 }
 
+template <int LPR, int P, bool VEC, typename T>
+hipError_t multistep_go(const MultiParams& mp, int units, int dv, hipStream_t st) {
+    constexpr int RPP = 256 / LPR;
+    dim3 grid(units, (dv + P * RPP - 1) / (P * RPP));
+    hipLaunchKernelGGL((gdr_multistep_kernel<LPR, P, VEC, T>), grid, dim3(256), 0, st, mp);
+    return hipGetLastError();
+}
+
+template <int LPR, bool VEC, typename T>
+hipError_t multistep_pick_p(const MultiParams& mp, int units, int dv, hipStream_t st) {
+    constexpr int RPP = 256 / LPR;
+    const int passes = (dv + RPP - 1) / RPP;
+    if (passes >= 4) return multistep_go<LPR, 4, VEC, T>(mp, units, dv, st);
+    if (passes == 3 || passes == 2) return multistep_go<LPR, 2, VEC, T>(mp, units, dv, st);
+    return multistep_go<LPR, 1, VEC, T>(mp, units, dv, st);
+}
+
+template <bool VEC, typename T>
+hipError_t multistep_pick_lpr(const MultiParams& mp, int units, int dk, int dv, hipStream_t st) {
+    switch (lanes_per_row(dk)) {
+        case 2: return multistep_pick_p<2, VEC, T>(mp, units, dv, st);
+        case 4: return multistep_pick_p<4, VEC, T>(mp, units, dv, st);
+        case 8: return multistep_pick_p<8, VEC, T>(mp, units, dv, st);
+        default: return multistep_pick_p<16, VEC, T>(mp, units, dv, st);
+    }
+}
+
 template <bool VEC, typename T>
 hipError_t recurrent_pick_lpr(const SeqParams& sp, int units, int dk, int dv, hipStream_t st) {
     const int lpr = lanes_per_row(dk);
@@ -278,6 +399,20 @@ hipError_t launch_decode(const rhz_gdr_decode_args& a, hipStream_t st) {
                    : decode_pick_lpr<false, float>(sp, units, a.d_k, a.d_v, st);
     return vec ? decode_pick_lpr<true, uint16_t>(sp, units, a.d_k, a.d_v, st)
                : decode_pick_lpr<false, uint16_t>(sp, units, a.d_k, a.d_v, st);
+}
+
+hipError_t launch_multistep(const rhz_gdr_multistep_args& a, hipStream_t st) {
+    MultiParams mp{a.q, a.k, a.v, a.gate, a.beta, a.state, a.states, a.o,
+                   a.steps, a.heads, a.d_k, a.d_v, a.gate_kind == RHZ_GATE_ALPHA};
+    const int units = a.batch * a.heads;
+    const size_t ea = a.dtype == RHZ_F32 ? 16 : 8;
+    const bool vec = (a.d_k % 4 == 0) && aligned(a.q, ea) && aligned(a.k, ea) && aligned(a.state, 16) &&
+                     aligned(a.states, 16);
+    if (a.dtype == RHZ_F32)
+        return vec ? multistep_pick_lpr<true, float>(mp, units, a.d_k, a.d_v, st)
+                   : multistep_pick_lpr<false, float>(mp, units, a.d_k, a.d_v, st);
+    return vec ? multistep_pick_lpr<true, uint16_t>(mp, units, a.d_k, a.d_v, st)
+               : multistep_pick_lpr<false, uint16_t>(mp, units, a.d_k, a.d_v, st);
 }
 
 hipError_t launch_recurrent(const rhz_gdr_prefill_args& a, hipStream_t st) {

@@ -149,6 +149,41 @@ def decode_step(q, k, v, g=None, beta=None, *, alpha=None, state, out=None, stre
     return o
 
 
+def multistep_args(q, k, v, gate, beta, gate_kind, state, states, o) -> _abi.MultistepArgs:
+    B, n, H, dk = q.shape
+    a = _abi.MultistepArgs()
+    a.batch, a.steps, a.heads, a.d_k, a.d_v = B, n, H, dk, v.shape[-1]
+    a.dtype = _DTYPES[q.dtype]
+    a.gate_kind = gate_kind
+    a.q, a.k, a.v, a.gate, a.beta = _ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta)
+    a.state, a.states, a.o = _ptr(state), _ptr(states), _ptr(o)
+    return a
+
+
+def multistep(q, k, v, g=None, beta=None, *, alpha=None, state, out=None, states=None,
+              stream=None):
+    """n consecutive positions for every (b, h) from ``state`` (read only).
+
+    q, k [B, n, H, d_k]; v [B, n, H, d_v]; gates [B, n, H].  Returns
+    (o [B, n, H, d_v], states [B, n, H, d_v, d_k]) with the state after each
+    position.  A segment change at position t is ``alpha[:, t] = 0``.
+    """
+    gate, gate_kind = _gate(g, alpha)
+    B, n, H, dk = q.shape
+    dv = v.shape[-1]
+    if (k.shape != q.shape or v.shape[:3] != (B, n, H) or gate.shape != (B, n, H)
+            or beta.shape != (B, n, H)):
+        raise ValueError("multistep shapes: q,k [B,n,H,dk], v [B,n,H,dv], gate/beta [B,n,H]")
+    if tuple(state.shape) != (B, H, dv, dk) or state.dtype != torch.float32:
+        raise ValueError("state must be fp32 [B,H,d_v,d_k]")
+    o = out if out is not None else torch.empty((B, n, H, dv), dtype=q.dtype, device=q.device)
+    if states is None:
+        states = torch.empty((B, n, H, dv, dk), dtype=torch.float32, device=q.device)
+    args = multistep_args(q, k, v, gate, beta, gate_kind, state, states, o)
+    _abi.check(_abi.lib().rhz_gdr_multistep(byref(args), _stream(stream)))
+    return o, states
+
+
 _FILL = {"normal": _abi.FILL_NORMAL, "unit_rows": _abi.FILL_UNIT_ROWS,
          "sigmoid": _abi.FILL_SIGMOID, "neg_softplus": _abi.FILL_NEG_SOFTPLUS}
 _FILL_DTYPES = {torch.float64: _abi.F64, torch.float32: _abi.F32, torch.bfloat16: _abi.BF16}
@@ -165,6 +200,7 @@ def philox_fill(kind: str, seed: int, stream_id: int, shape, dtype=torch.float32
 
 
 def query_support(op: str, dtype, d_k: int, d_v: int, algo: str = "auto") -> int:
-    """rhz_gdr_query_support status for op 'scan' or 'step'."""
-    ops = {"scan": _abi.OP_DELTA_SCAN, "step": _abi.OP_DELTA_STEP}
+    """rhz_gdr_query_support status for op 'scan', 'step' or 'multistep'."""
+    ops = {"scan": _abi.OP_DELTA_SCAN, "step": _abi.OP_DELTA_STEP,
+           "multistep": _abi.OP_DELTA_MULTISTEP}
     return _abi.lib().rhz_gdr_query_support(ops[op], _DTYPES[dtype], d_k, d_v, _ALGOS[algo])

@@ -50,7 +50,10 @@ def test_identity_and_status_strings(lib):
     (_abi.OP_DELTA_STEP, _abi.F32, 128, 128, _abi.ALGO_AUTO, _abi.OK),
     (_abi.OP_DELTA_STEP, _abi.F32, 128, 128, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
     (_abi.OP_DELTA_STEP, _abi.F32, 128, 2048, _abi.ALGO_AUTO, _abi.ERR_UNSUPPORTED),
+    (_abi.OP_DELTA_MULTISTEP, _abi.BF16, 128, 128, _abi.ALGO_AUTO, _abi.OK),
+    (_abi.OP_DELTA_MULTISTEP, _abi.F32, 64, 64, _abi.ALGO_CHUNKED, _abi.ERR_UNSUPPORTED),
     (7, _abi.F32, 128, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
+    (3, _abi.F32, 128, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
     (_abi.OP_DELTA_STEP, _abi.F64, 128, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
     (_abi.OP_DELTA_STEP, _abi.F32, 0, 128, _abi.ALGO_AUTO, _abi.ERR_INVALID_ARG),
     (_abi.OP_DELTA_SCAN, _abi.F32, 128, 128, 9, _abi.ERR_INVALID_ARG),
@@ -161,6 +164,43 @@ def test_decode_validation(over, status, msg):
     assert _abi.lib().rhz_gdr_decode_step(byref(args), None) == status
     assert msg in _abi.last_error()
     assert _abi.lib().rhz_gdr_decode_step(None, None) == _abi.ERR_INVALID_ARG
+
+
+def _multistep(**over):
+    a = _abi.MultistepArgs()
+    a.batch, a.steps, a.heads, a.d_k, a.d_v = 64, 8, 16, 128, 128
+    a.dtype, a.gate_kind = _abi.F32, _abi.GATE_ALPHA
+    for name in ("q", "k", "v", "gate", "beta", "state", "states", "o"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(batch=0), _abi.ERR_INVALID_ARG, "batch"),
+    (dict(steps=0), _abi.ERR_INVALID_ARG, "steps"),
+    (dict(heads=0), _abi.ERR_INVALID_ARG, "heads"),
+    (dict(d_k=0), _abi.ERR_INVALID_ARG, "d_k"),
+    (dict(d_v=-1), _abi.ERR_INVALID_ARG, "d_v"),
+    (dict(dtype=_abi.F64), _abi.ERR_INVALID_ARG, "dtype"),
+    (dict(gate_kind=3), _abi.ERR_INVALID_ARG, "gate_kind"),
+    (dict(steps=_abi.MULTISTEP_MAX + 1), _abi.ERR_UNSUPPORTED, "steps"),
+    (dict(d_k=257), _abi.ERR_UNSUPPORTED, "256"),
+    (dict(d_v=1025), _abi.ERR_UNSUPPORTED, "1024"),
+    (dict(batch=1 << 20, steps=64, heads=64), _abi.ERR_INVALID_ARG, "2^31"),
+    (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
+    (dict(state=None), _abi.ERR_INVALID_ARG, "state is NULL"),
+    (dict(states=None), _abi.ERR_INVALID_ARG, "states is NULL"),
+    (dict(o=None), _abi.ERR_INVALID_ARG, "o is NULL"),
+    (dict(v=A + 2), _abi.ERR_INVALID_ARG, "v is not aligned"),
+    (dict(states=A + 2), _abi.ERR_INVALID_ARG, "4-byte aligned"),
+])
+def test_multistep_validation(over, status, msg):
+    args = _multistep(**over)
+    assert _abi.lib().rhz_gdr_multistep(byref(args), None) == status
+    assert msg in _abi.last_error()
+    assert _abi.lib().rhz_gdr_multistep(None, None) == _abi.ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("args,msg", [
