@@ -4,6 +4,8 @@
 
 Every .hip / .cpp file under rhizome_amd/csrc is compiled separately (in
 parallel) and linked into rhizome_amd/librhizome_gdr.so next to this file.
+The C++ restatement of the reference's delta.rs API (rhizome_amd/host) is
+linked against it into rhizome_amd/librhizome_ops.so.
 """
 from __future__ import annotations
 
@@ -18,6 +20,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librhizome_gdr.so")
+HOST = os.path.join(HERE, "host")
+OPS_LIB = os.path.join(HERE, "librhizome_ops.so")
 ARCH = "gfx950"
 
 # Packed-FP32 instructions stay off (the compiler emits none of
@@ -64,7 +68,30 @@ def build(jobs: int | None = None) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_ops()
     return LIB
+
+
+def build_ops() -> str:
+    """librhizome_ops.so: the delta.rs-shaped C++ API over librhizome_gdr.so."""
+    objs = []
+    for f in sorted(os.listdir(HOST)):
+        if f.endswith(".cpp"):
+            obj = os.path.join(OBJ, "host_" + f + ".o")
+            cmd = [hipcc(), "-O2", "-fPIC", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+                   "-I", HOST, "-c", os.path.join(HOST, f), "-o", obj]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed on host/{f}:\n{res.stderr}")
+            objs.append(obj)
+    tmp = OPS_LIB + ".tmp"
+    cmd = [hipcc(), "-shared", "-fPIC", "-o", tmp] + objs + [
+        "-L", HERE, "-lrhizome_gdr", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of librhizome_ops.so failed:\n{res.stderr}")
+    os.replace(tmp, OPS_LIB)
+    return OPS_LIB
 
 
 if __name__ == "__main__":
