@@ -311,20 +311,24 @@ __device__ __forceinline__ void signal(int* cnt) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     asm volatile("" ::: "memory");
 }
-__device__ __forceinline__ void wait_ge(int* cnt, int target);
-// Both scan waves have finished chunk x.
-__device__ __forceinline__ void wait_scanned(Sync& sy, int x) {
-    wait_ge(&sy.scanned[0], x + 1);
-    wait_ge(&sy.scanned[1], x + 1);
-}
-__device__ __forceinline__ void wait_ge(int* cnt, int target) {
+// Waits until every counter c[i] >= t[i] (a target <= 0 holds at once).
+// Each poll reads all N counters back to back, so a wait costs one LDS
+// round trip however many counters it checks.
+template <int N>
+__device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) {
     for (int spin = 0; spin < kSpinLimit; ++spin) {
-        const int v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (__builtin_amdgcn_readfirstlane(v) >= target) break;
+        int v[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = __hip_atomic_load(c[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) ok &= __builtin_amdgcn_readfirstlane(v[i]) >= t[i];
+        if (ok) break;
         __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
 }
+__device__ __forceinline__ void wait_ge(int* cnt, int target) { wait_all<1>({cnt}, {target}); }
 
 // Shared memory of one workgroup.  Buffers indexed [2] are double-buffered
 // by chunk parity.  T and P hold zeros above the diagonal blocks for the
@@ -643,11 +647,9 @@ template <int DK, int B>
 __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
-    wait_ge(&sm.sync.staged, 4 * (x + 1));
-    if (x >= 2) {  // T[B] was read by the scan and written by both waves for chunk x - 2
-        wait_scanned(sm.sync, x - 2);
-        wait_ge(&sm.sync.tfull, 2 * (x - 1));
-    }
+    // K[B] staged; T[B] was read by the scan and written by both waves for chunk x - 2
+    Sync& sy = sm.sync;
+    wait_all<4>({&sy.staged, &sy.scanned[0], &sy.scanned[1], &sy.tfull}, {4 * (x + 1), x - 1, x - 1, 2 * (x - 1)});
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
@@ -672,8 +674,8 @@ template <int DK, int B>
 __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
-    wait_ge(&sm.sync.staged, 4 * (x + 1));
-    wait_ge(&sm.sync.tfull, 2 * x);  // A (one buffer) was read by T's blocks of chunk x - 1
+    // K[B] staged; A (one buffer) was read by T's blocks of chunk x - 1
+    wait_all<2>({&sm.sync.staged, &sm.sync.tfull}, {4 * (x + 1), 2 * x});
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
@@ -735,12 +737,10 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
 template <int DK, int B, int LW>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
-    if (x >= 2) {  // buffer B held chunk x - 2: every reader of it is done
-        wait_scanned(sm.sync, x - 2);
-        wait_ge(&sm.sync.pdone, 4 * (x - 1));
-        wait_ge(&sm.sync.tdiag, x - 1);
-        wait_ge(&sm.sync.aoff, x - 1);
-    }
+    // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
+    Sync& sy = sm.sync;
+    wait_all<5>({&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
+                {x - 1, x - 1, 4 * (x - 1), x - 1, x - 1});
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
     stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
     signal(&sm.sync.staged);
@@ -889,8 +889,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         for (int tb2 = 0; tb2 < 4; ++tb2) OQ[tb2] *= gq[tb2] * fo;
     }
     // ---- U = T Rhat, O^T += U^T P^T, S update.
-    wait_ge(&sm.sync.tfull, 2 * (c + 1));
-    wait_ge(&sm.sync.pdone, 4 * (c + 1));
+    wait_all<2>({&sm.sync.tfull, &sm.sync.pdone}, {2 * (c + 1), 4 * (c + 1)});
     {
         const int F1 = st.F + er;
         // T rows (both 32-token halves for rows >= 32), P rows, decays.
