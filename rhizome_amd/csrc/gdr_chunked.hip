@@ -302,7 +302,7 @@ struct Sync {
     int aoff;    // wave 3 (1 per chunk): A below the diagonal
     int tfull;   // waves 2, 3 (2 per chunk): T complete
     int pdone;   // loader waves (4 per chunk): P
-    int scanned[2];  // scan wave w (1 per chunk): chunk finished, its buffers free
+    int scanned[2];  // scan wave w (1 per chunk): its last read of the chunk's buffers returned
 };
 constexpr int kSpinLimit = 1 << 20;
 
@@ -313,7 +313,8 @@ __device__ __forceinline__ void signal(int* cnt) {
 }
 // Waits until every counter c[i] >= t[i] (a target <= 0 holds at once).
 // Each poll reads all N counters back to back, so a wait costs one LDS
-// round trip however many counters it checks.
+// round trip however many counters it checks; polls follow each other
+// without sleeping (measured faster than s_sleep between polls).
 template <int N>
 __device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) {
     for (int spin = 0; spin < kSpinLimit; ++spin) {
@@ -324,7 +325,6 @@ __device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) 
 #pragma unroll
         for (int i = 0; i < N; ++i) ok &= __builtin_amdgcn_readfirstlane(v[i]) >= t[i];
         if (ok) break;
-        __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
 }
@@ -936,8 +936,14 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
             }
         };
         constexpr int kAhead = NJ < 2 ? NJ : 2;
+        // The last read of buffer B is issued in S-update step kLastRead
+        // (before the loop when negative); once it has returned the buffer is
+        // free, so the chunk is counted there, ahead of the remaining MFMAs,
+        // the output stores and the state maximum.
+        constexpr int kLastRead = NJ - 1 - kAhead;
 #pragma unroll
         for (int jb = 0; jb < kAhead; ++jb) kt_load(jb);
+        if constexpr (kLastRead < 0) signal(&sm.sync.scanned[w]);
         // O^T[tb2] lane (n, g): token 16 tb2 + n, state rows orow + 0..3
         f32x4 O[4];
 #pragma unroll
@@ -950,6 +956,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
 #pragma unroll
         for (int jb = 0; jb < NJ; ++jb) {
             if (jb + kAhead < NJ) kt_load(jb + kAhead);
+            if (jb == kLastRead) signal(&sm.sync.scanned[w]);
             f32x4 acc = st.S[jb] * sd;
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
@@ -975,7 +982,6 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         st.F = F1;
         st.smax = state_max(st);
     }
-    signal(&sm.sync.scanned[w]);
 }
 
 // ------------------------------------------------------------ fused kernel
