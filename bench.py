@@ -71,6 +71,7 @@ def decode_bytes(batch, heads, dk, dv) -> float:
 PROFILES = {
     "prefill": "gdr_chunk_kernel_128_prefill_b4_h16_t4096_d128.md",
     "decode": "gdr_decode_kernel_decode_b256_h16_d128.md",
+    "multistep": "gdr_multistep_kernel_b256_h16_d128_n8.md",
 }
 
 
@@ -353,6 +354,7 @@ def main() -> int:
                       "roofline": {"bound": "hbm", "achieved": mbytes / (mms * 1e-3) / 1e9,
                                    "peak": PEAK_HBM_GBS,
                                    "frac": mbytes / (mms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                   "traffic": traffic_from_profiles("multistep"),
                                    "kernel": "gdr_multistep_kernel<8,4,true,float>",
                                    "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
         "device": torch.cuda.get_device_name(0),
