@@ -355,7 +355,7 @@ def main() -> int:
                                    "peak": PEAK_HBM_GBS,
                                    "frac": mbytes / (mms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                    "traffic": traffic_from_profiles("multistep"),
-                                   "kernel": "gdr_multistep_kernel<8,4,true,float>",
+                                   "kernel": "gdr_multistep_kernel<8,2,true,float>",
                                    "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
         "device": torch.cuda.get_device_name(0),
     }

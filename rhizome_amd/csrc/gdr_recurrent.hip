@@ -85,15 +85,23 @@ __device__ __forceinline__ void load_slice(const T* row, int li, int n, float (&
     }
 }
 
-template <int LPR, bool VEC>
+// NT: non-temporal stores (streaming output that this kernel does not read
+// back, such as the multistep snapshots).
+template <int LPR, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_slice(float* row, int li, int n, const float (&x)[16]) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int col = c * 4 * LPR + 4 * li;
         if (VEC) {
-            if (col < n)
-                *reinterpret_cast<float4*>(row + col) =
-                    make_float4(x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+            if (col < n) {
+                if (NT) {
+                    const f32x4 val = {x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
+                    __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(row + col));
+                } else {
+                    *reinterpret_cast<float4*>(row + col) =
+                        make_float4(x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+                }
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
             if (r < dv) {
-                store_slice<LPR, VEC>(snap + (long)r * dk, li, dk, s[pp]);
+                store_slice<LPR, VEC, true>(snap + (long)r * dk, li, dk, s[pp]);
                 if (li == 0) Elem<T>::store(op, th * dv + r, oi);
             }
         }
@@ -357,9 +365,9 @@ hipError_t multistep_go(const MultiParams& mp, int units, int dv, hipStream_t st
 template <int LPR, bool VEC, typename T>
 hipError_t multistep_pick_p(const MultiParams& mp, int units, int dv, hipStream_t st) {
     constexpr int RPP = 256 / LPR;
+    // two passes per thread: measured faster than four for the snapshot writes
     const int passes = (dv + RPP - 1) / RPP;
-    if (passes >= 4) return multistep_go<LPR, 4, VEC, T>(mp, units, dv, st);
-    if (passes == 3 || passes == 2) return multistep_go<LPR, 2, VEC, T>(mp, units, dv, st);
+    if (passes >= 2) return multistep_go<LPR, 2, VEC, T>(mp, units, dv, st);
     return multistep_go<LPR, 1, VEC, T>(mp, units, dv, st);
 }
 
