@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void gdr_decode_kernel(StepParams p) {
             const float oi = alpha * sq + c * kq;
 #pragma unroll
             for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
-            store_slice<LPR, VEC>(S + (long)r * dk, li, dk, s[pp]);
+            store_slice<LPR, VEC, true>(S + (long)r * dk, li, dk, s[pp]);
             if (li == 0) Elem<T>::store(o, r, oi);
         }
     }
