@@ -6,8 +6,9 @@ B=4, H=16, T=4096, d_k=d_v=128, bf16 q/k/v, fp32 gates/state, chunk 64 --
 one step = one rhz_gdr_prefill over the whole batch (all heads), inputs
 resident in HBM.  Alongside (`decode`): the decode state update on B=256,
 H=16, d=128, fp32 state, one rhz_gdr_decode_step launch per step over 64
-steps, as HBM GB/s; and (`multistep`) rhz_gdr_multistep over 8 positions on
-the same shape, as HBM GB/s.
+steps, as HBM GB/s; (`multistep`) rhz_gdr_multistep over 8 positions on
+the same shape, as HBM GB/s; and (`prologue_epilogue`) the conv1d, prepare and
+per-head RMSNorm ops on the prefill workload's tokens, as HBM GB/s.
 
 Inputs are synthetic and seeded: the reference's Philox-4x32-10 streams
 (q=1, k=2, v=3, beta=4, g=5, state=6), generated on the device by
@@ -206,6 +207,50 @@ def bench_multistep(torch, steps, warmup):
     return ms, multistep_bytes(B, H, dk, dv, n)
 
 
+def bench_aux(torch, steps, warmup):
+    """The prologue / epilogue ops on config 1's 16384 tokens (H=16, d=128,
+    bf16): conv1d over q, k, v's 6144 channels, prepare, per-head RMSNorm.
+    GB/s counts each tensor read or written once."""
+    import rhizome_amd
+
+    T, H, d = PREFILL["batch"] * PREFILL["seq_len"], PREFILL["heads"], PREFILL["d_k"]
+    C = 3 * H * d
+    bf16, f32 = torch.bfloat16, torch.float32
+    x = rhizome_amd.philox_fill("normal", 0, 11, (T, C), bf16)
+    w = rhizome_amd.philox_fill("normal", 0, 12, (C, 4), f32, std=0.5)
+    cb = rhizome_amd.philox_fill("normal", 0, 13, (C,), f32)
+    y = torch.empty_like(x)
+    q = rhizome_amd.philox_fill("normal", 0, 14, (T, H, d), bf16)
+    k = rhizome_amd.philox_fill("normal", 0, 15, (T, H, d), bf16)
+    lg = rhizome_amd.philox_fill("normal", 0, 16, (T, H), f32)
+    a = rhizome_amd.philox_fill("normal", 0, 17, (H,), f32)
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    o = rhizome_amd.philox_fill("normal", 0, 18, (T, H, d), bf16)
+    sc = rhizome_amd.philox_fill("normal", 0, 19, (d,), f32)
+    on = torch.empty_like(o)
+    stream = torch.cuda.current_stream()
+    jobs = {
+        "conv1d": (lambda: rhizome_amd.causal_conv1d(x.view(1, T, C), w, cb, out=y.view(1, T, C)),
+                   2 * T * C * 2 + C * 20, "conv1d_kernel<bf16>", "B=1 T=16384, 6144 channels"),
+        "prepare": (lambda: rhizome_amd.prepare(q, k, lg, lg, a, q_out=qo, k_out=ko),
+                    4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<32,4,bf16>",
+                    "16384 tokens, H=16, d_k=128"),
+        "rmsnorm": (lambda: rhizome_amd.rmsnorm_heads(o, sc, 1e-6, out=on), 2 * T * H * d * 2 + d * 4,
+                    "rmsnorm_kernel<32,4,bf16>", "16384 x 16 rows of 128"),
+    }
+    out = {}
+    for name, (fn, nbytes, kernel, shape) in jobs.items():
+        for _ in range(warmup):
+            fn()
+        ms = time_region(torch, stream, fn, steps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"value": gbs, "unit": "GB/s", "ms_per_step": ms, "workload": shape,
+                     "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
+                                  "frac": gbs / PEAK_HBM_GBS, "kernel": kernel,
+                                  "bytes_per_launch": float(nbytes), "launch_us": ms * 1e3}}
+    return out
+
+
 def cpu_baseline(pre_host, dec_host):
     """f64 oracle on this host: reference three-pass step with per-call allocations."""
     import numpy as np
@@ -303,6 +348,7 @@ def main() -> int:
     ms, flops, algo_bytes, pre_host = bench_prefill(torch, args.steps, args.warmup)
     dms, dbytes, dec_host = bench_decode(torch, args.warmup)
     mms, mbytes = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
+    aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
     if args.calibration_copy:
         calibration_copy(torch)
     c = PREFILL
@@ -357,6 +403,7 @@ def main() -> int:
                                    "traffic": traffic_from_profiles("multistep"),
                                    "kernel": "gdr_multistep_kernel<8,2,true,float>",
                                    "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
+        "prologue_epilogue": aux,
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu_baseline:

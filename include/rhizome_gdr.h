@@ -180,6 +180,73 @@ rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* args, void* stream);
 /* Gated delta-rule multistep (see rhz_gdr_multistep_args). */
 rhz_status rhz_gdr_multistep(const rhz_gdr_multistep_args* args, void* stream);
 
+/* ---- Local-block prologue and epilogue around the op (SPEC.md:53-63) ---- */
+
+/* Causal depthwise conv1d of width 4 over packed or dense sequences, with a
+ * 3-sample carried state per (sequence, channel).  Per channel, the reference
+ * step (causal_conv1d_step, delta.rs:232-243) applied along each sequence:
+ *     y_t = w[0] x_{t-3} + w[1] x_{t-2} + w[2] x_{t-1} + w[3] x_t + bias
+ * where x before the sequence start comes from initial_state (oldest first)
+ * or is zero; final_state receives the last three inputs (the state after the
+ * last step).  A sequence start resets the conv state as SPEC.md:61-63 asks. */
+typedef struct rhz_conv1d_args {
+    int32_t batch;    /* dense: B;  packed: number of sequences N (>= 1) */
+    int32_t seq_len;  /* dense: T;  packed: total tokens (>= 0) */
+    int32_t channels; /* C >= 1 */
+    int32_t dtype;    /* rhz_dtype of x and y (RHZ_F32 or RHZ_BF16) */
+    const void* x;              /* [tokens, C] */
+    const float* weight;        /* [C, 4] */
+    const float* bias;          /* [C], or NULL for zero */
+    const int32_t* cu_seqlens;  /* [N+1] or NULL (dense) */
+    const float* initial_state; /* [batch, C, 3] oldest first, or NULL for zeros */
+    float* final_state;         /* [batch, C, 3], or NULL */
+    void* y;                    /* [tokens, C], dtype; must not overlap x */
+} rhz_conv1d_args;
+
+rhz_status rhz_causal_conv1d(const rhz_conv1d_args* args, void* stream);
+
+/* The op's inputs from the projections (SPEC.md:53-56), per (token, head):
+ *     q := l2norm(q) * q_scale,  k := l2norm(k)       (elementwise.rs:125-128)
+ *     beta := sigmoid(beta_logit)                     (elementwise.rs:5-12)
+ *     g := -softplus(a_log[h]) * softplus(alpha_logit), alpha = exp(g)
+ *                                                     (elementwise.rs:36-42)
+ * q_out / k_out may alias q_in / k_in.  g is the log-decay that
+ * rhz_gdr_prefill / rhz_gdr_decode_step take with RHZ_GATE_LOG_ALPHA. */
+typedef struct rhz_gdr_prepare_args {
+    int32_t tokens;   /* >= 0 */
+    int32_t heads;    /* H >= 1 */
+    int32_t d_k;      /* 1..256 */
+    int32_t dtype;    /* rhz_dtype of q and k, in and out */
+    float q_scale;    /* SPEC.md:53: sqrt(d_k) */
+    const void* q_in;          /* [tokens, H, d_k] */
+    const void* k_in;          /* [tokens, H, d_k] */
+    void* q_out;               /* [tokens, H, d_k] */
+    void* k_out;               /* [tokens, H, d_k] */
+    const float* beta_logit;   /* [tokens, H] */
+    const float* alpha_logit;  /* [tokens, H] */
+    const float* a_log;        /* [H] */
+    float* beta;               /* [tokens, H] out */
+    float* g;                  /* [tokens, H] out */
+} rhz_gdr_prepare_args;
+
+rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* args, void* stream);
+
+/* RMSNorm of every row of `dim` values with a learned scale, as the
+ * per-head norm of the op's output (groupnorm_heads / rmsnorm,
+ * norm.rs:8-13, 48-59): y = x / sqrt(mean(x^2) + eps) * scale.  y may alias
+ * x. */
+typedef struct rhz_rmsnorm_args {
+    int32_t rows;     /* tokens * heads, >= 0 */
+    int32_t dim;      /* 1..1024 */
+    int32_t dtype;    /* rhz_dtype of x and y */
+    float eps;        /* norm.rs:4: 1e-6 */
+    const void* x;        /* [rows, dim] */
+    const float* scale;   /* [dim] */
+    void* y;              /* [rows, dim] */
+} rhz_rmsnorm_args;
+
+rhz_status rhz_rmsnorm_heads(const rhz_rmsnorm_args* args, void* stream);
+
 /* Seeded synthetic inputs on the device, from the reference's Philox-4x32-10
  * (crates/ops/src/rng.rs:43-90; elementwise.rs:5-12, 36-42, 125-128).
  * Element e of the output takes normal #e of stream (seed, stream_id): the

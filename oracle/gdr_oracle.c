@@ -13,6 +13,8 @@
  *   orc_gated_delta_scan_chunked crates/ops/src/delta.rs:159-197
  *   orc_gated_delta_multistep   crates/ops/src/delta.rs:202-230
  *   orc_causal_conv1d_step      crates/ops/src/delta.rs:236-243
+ *   orc_conv1d_batched          the same step along packed sequences and channels
+ *   orc_rmsnorm_rows            crates/ops/src/norm.rs:8-13 (and 48-59 per head)
  *   orc_make_inputs             crates/ops/src/delta.rs:254-280 (test fixture builder)
  *   Philox-4x32-10              crates/ops/src/rng.rs:7-90
  *   orc_sigmoid / orc_softplus / orc_l2norm
@@ -352,6 +354,39 @@ double orc_causal_conv1d_step(double state[3], const double weight[4], double x,
     state[1] = state[2];
     state[2] = x;
     return y;
+}
+
+/* causal_conv1d_step (delta.rs:236-243) along every sequence of a pack and
+ * every channel: x [tokens, C], weight [C][4], bias [C] or NULL, state
+ * [n][C][3] from init (or zeros) at each sequence start, final state into
+ * fin (may be NULL).  Tokens outside every sequence are not written. */
+void orc_conv1d_batched(int64_t n_seqs, const int64_t* cu_seqlens, int64_t C, const double* x,
+                        const double* weight, const double* bias, const double* init, double* y,
+                        double* fin)
+{
+    for (int64_t s = 0; s < n_seqs; ++s) {
+        for (int64_t c = 0; c < C; ++c) {
+            double st[3] = {0.0, 0.0, 0.0};
+            if (init) memcpy(st, init + (s * C + c) * 3, sizeof st);
+            for (int64_t t = cu_seqlens[s]; t < cu_seqlens[s + 1]; ++t)
+                y[t * C + c] = orc_causal_conv1d_step(st, weight + 4 * c, x[t * C + c], bias ? bias[c] : 0.0);
+            if (fin) memcpy(fin + (s * C + c) * 3, st, sizeof st);
+        }
+    }
+}
+
+/* norm.rs:8-13 on every row of `dim` values (groupnorm_heads, norm.rs:48-59,
+ * is this on each head's slice). */
+void orc_rmsnorm_rows(int64_t rows, int64_t dim, const double* x, const double* scale, double eps, double* y)
+{
+    for (int64_t r = 0; r < rows; ++r) {
+        const double* xr = x + r * dim;
+        double ss = 0.0;
+        for (int64_t i = 0; i < dim; ++i) ss += xr[i] * xr[i];
+        double ms = ss / (double)dim;
+        double inv = 1.0 / sqrt(ms + eps);
+        for (int64_t i = 0; i < dim; ++i) y[r * dim + i] = xr[i] * inv * scale[i];
+    }
 }
 
 /* delta.rs:254-280 (the reference's test-fixture builder): stream 17 gives

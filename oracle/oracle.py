@@ -62,6 +62,9 @@ def lib():
         L.orc_gated_delta_multistep.restype = c_int64
         L.orc_causal_conv1d_step.argtypes = [_dp, _dp, c_double, c_double]
         L.orc_causal_conv1d_step.restype = c_double
+        L.orc_conv1d_batched.argtypes = [c_int64, POINTER(c_int64), c_int64, _dp, _dp, c_void_p,
+                                         c_void_p, _dp, c_void_p]
+        L.orc_rmsnorm_rows.argtypes = [c_int64, c_int64, _dp, _dp, c_double, _dp]
         L.orc_make_inputs.argtypes = [c_int64, c_int64, c_uint64, _dp, _dp, _dp, _dp, _dp]
         L.orc_gdr_steps_rect.argtypes = [
             c_int64, c_int64, c_int64, _dp, c_int64, _dp, c_int64, _dp, c_int64,
@@ -232,6 +235,49 @@ def causal_conv1d_step(state: np.ndarray, weight, x: float, bias: float) -> floa
     assert state.dtype == np.float64 and state.size == 3
     w = _f64(weight)
     return lib().orc_causal_conv1d_step(_p(state), _p(w), x, bias)
+
+
+def conv1d_batched(cu_seqlens, x, weight, bias=None, init=None):
+    """causal_conv1d_step (delta.rs:236-243) along packed sequences and channels.
+
+    x [tokens, C]; weight [C, 4]; bias [C] or None; init [n, C, 3] or None.
+    Returns (y [tokens, C], final state [n, C, 3]); tokens outside every
+    sequence stay NaN."""
+    x, weight = _f64(x), _f64(weight)
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int64)
+    n = cu.size - 1
+    tokens, C = x.shape
+    y = np.full((tokens, C), np.nan)
+    fin = np.zeros((n, C, 3))
+    b = _f64(bias) if bias is not None else None
+    st = _f64(init) if init is not None else None
+    lib().orc_conv1d_batched(n, cu.ctypes.data_as(POINTER(c_int64)), C, _p(x), _p(weight),
+                             _pn(b), _pn(st), _p(y), _p(fin))
+    return y, fin
+
+
+def rmsnorm_rows(x, scale, eps: float = 1e-6) -> np.ndarray:
+    """rmsnorm (norm.rs:8-13) of every row of x [rows, dim]."""
+    x, scale = _f64(x), _f64(scale)
+    rows, dim = x.shape
+    y = np.zeros_like(x)
+    lib().orc_rmsnorm_rows(rows, dim, _p(x), _p(scale), eps, _p(y))
+    return y
+
+
+def prepare(q, k, beta_logit, alpha_logit, a_log, q_scale: float):
+    """The op's inputs from the projections (SPEC.md:53-56) per (token, head):
+    l2norm(q) * q_scale, l2norm(k), sigmoid(beta_logit),
+    g = -softplus(a_log[h]) * softplus(alpha_logit).  q, k [tokens, H, d];
+    logits [tokens, H]; a_log [H]."""
+    q, k = _f64(q).copy(), _f64(k).copy()
+    T, H, d = q.shape
+    l2norm_rows(q.reshape(T * H, d), d, q_scale)
+    l2norm_rows(k.reshape(T * H, d), d, 1.0)
+    beta = sigmoid_vec(_f64(beta_logit).ravel()).reshape(T, H)
+    sp_a = -neg_softplus_vec(_f64(a_log))
+    sp_l = -neg_softplus_vec(_f64(alpha_logit).ravel()).reshape(T, H)
+    return q, k, beta, -sp_a[None, :] * sp_l
 
 
 def make_inputs(t: int, d: int, seed: int) -> dict:

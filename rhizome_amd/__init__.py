@@ -5,6 +5,8 @@ The compute lives in librhizome_gdr.so (hand-written HIP kernels, built by
 end.  Importing the package does not load the library; the first call does,
 and raises if the library is missing.
 """
-from .gdr import decode_step, multistep, philox_fill, prefill, query_support  # noqa: F401
+from .gdr import (causal_conv1d, decode_step, multistep, philox_fill, prefill,  # noqa: F401
+                  prepare, query_support, rmsnorm_heads)
 
-__all__ = ["prefill", "decode_step", "multistep", "philox_fill", "query_support"]
+__all__ = ["prefill", "decode_step", "multistep", "causal_conv1d", "prepare", "rmsnorm_heads",
+           "philox_fill", "query_support"]

@@ -9,7 +9,8 @@ from __future__ import annotations
 import ctypes
 import os
 import re
-from ctypes import POINTER, Structure, c_char_p, c_double, c_int32, c_int64, c_size_t, c_uint64, c_void_p
+from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int32, c_int64, c_size_t,
+                    c_uint64, c_void_p)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -60,6 +61,31 @@ class MultistepArgs(Structure):
     ]
 
 
+class Conv1dArgs(Structure):
+    _fields_ = [
+        ("batch", c_int32), ("seq_len", c_int32), ("channels", c_int32), ("dtype", c_int32),
+        ("x", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("cu_seqlens", c_void_p),
+        ("initial_state", c_void_p), ("final_state", c_void_p), ("y", c_void_p),
+    ]
+
+
+class PrepareArgs(Structure):
+    _fields_ = [
+        ("tokens", c_int32), ("heads", c_int32), ("d_k", c_int32), ("dtype", c_int32),
+        ("q_scale", c_float),
+        ("q_in", c_void_p), ("k_in", c_void_p), ("q_out", c_void_p), ("k_out", c_void_p),
+        ("beta_logit", c_void_p), ("alpha_logit", c_void_p), ("a_log", c_void_p),
+        ("beta", c_void_p), ("g", c_void_p),
+    ]
+
+
+class RmsnormArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32), ("dim", c_int32), ("dtype", c_int32), ("eps", c_float),
+        ("x", c_void_p), ("scale", c_void_p), ("y", c_void_p),
+    ]
+
+
 class GdrError(RuntimeError):
     """A non-OK rhz_status, with the library's detail message."""
 
@@ -100,6 +126,12 @@ def lib():
         L.rhz_gdr_decode_step.restype = c_int32
         L.rhz_gdr_multistep.argtypes = [POINTER(MultistepArgs), c_void_p]
         L.rhz_gdr_multistep.restype = c_int32
+        L.rhz_causal_conv1d.argtypes = [POINTER(Conv1dArgs), c_void_p]
+        L.rhz_causal_conv1d.restype = c_int32
+        L.rhz_gdr_prepare.argtypes = [POINTER(PrepareArgs), c_void_p]
+        L.rhz_gdr_prepare.restype = c_int32
+        L.rhz_rmsnorm_heads.argtypes = [POINTER(RmsnormArgs), c_void_p]
+        L.rhz_rmsnorm_heads.restype = c_int32
         L.rhz_philox_fill.argtypes = [c_int32, c_uint64, c_uint64, c_int64, c_int32, c_double,
                                       c_double, c_int32, c_void_p, c_void_p]
         L.rhz_philox_fill.restype = c_int32

@@ -253,6 +253,70 @@ rhz_status rhz_gdr_multistep(const rhz_gdr_multistep_args* a, void* stream) {
     return hip_status(rhz::launch_multistep(*a, static_cast<hipStream_t>(stream)), "multistep launch");
 }
 
+namespace {
+bool misaligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a != 0; }
+}  // namespace
+
+rhz_status rhz_causal_conv1d(const rhz_conv1d_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->batch < 1) return fail(RHZ_ERR_INVALID_ARG, "batch must be >= 1 (got %d)", a->batch);
+    if (a->seq_len < 0) return fail(RHZ_ERR_INVALID_ARG, "seq_len must be >= 0 (got %d)", a->seq_len);
+    if (a->channels < 1) return fail(RHZ_ERR_INVALID_ARG, "channels must be >= 1 (got %d)", a->channels);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    const int64_t tokens = a->cu_seqlens ? a->seq_len : (int64_t)a->batch * a->seq_len;
+    if (tokens * a->channels > kMaxIndex || (int64_t)a->batch * a->channels * 3 > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "tokens * channels and batch * channels * 3 must stay below 2^31");
+    if (tokens > 0 && (!a->x || !a->y)) return fail(RHZ_ERR_INVALID_ARG, "x or y is NULL");
+    if (!a->weight) return fail(RHZ_ERR_INVALID_ARG, "weight is NULL");
+    const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+    if (misaligned(a->x, ea) || misaligned(a->y, ea))
+        return fail(RHZ_ERR_INVALID_ARG, "x or y is not aligned to its element size");
+    if (misaligned(a->weight, 4) || misaligned(a->bias, 4) || misaligned(a->initial_state, 4) ||
+        misaligned(a->final_state, 4) || misaligned(a->cu_seqlens, 4))
+        return fail(RHZ_ERR_INVALID_ARG, "fp32 and int32 tensors must be 4-byte aligned");
+    return hip_status(rhz::launch_conv1d(*a, static_cast<hipStream_t>(stream)), "conv1d launch");
+}
+
+rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->tokens < 0) return fail(RHZ_ERR_INVALID_ARG, "tokens must be >= 0 (got %d)", a->tokens);
+    if (a->heads < 1) return fail(RHZ_ERR_INVALID_ARG, "heads must be >= 1 (got %d)", a->heads);
+    if (a->d_k < 1) return fail(RHZ_ERR_INVALID_ARG, "d_k must be >= 1 (got %d)", a->d_k);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (a->d_k > 256) return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d exceeds the supported 256", a->d_k);
+    if ((int64_t)a->tokens * a->heads * a->d_k > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "tokens * heads * d_k exceeds 2^31 - 1");
+    if (a->tokens == 0) return ok();
+    const void* ptrs[] = {a->q_in, a->k_in, a->q_out, a->k_out, a->beta_logit, a->alpha_logit, a->a_log,
+                          a->beta, a->g};
+    const char* names[] = {"q_in", "k_in", "q_out", "k_out", "beta_logit", "alpha_logit", "a_log", "beta", "g"};
+    for (int i = 0; i < 9; ++i)
+        if (!ptrs[i]) return fail(RHZ_ERR_INVALID_ARG, "%s is NULL", names[i]);
+    const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+    for (int i = 0; i < 9; ++i)
+        if (misaligned(ptrs[i], i < 4 ? ea : 4)) return fail(RHZ_ERR_INVALID_ARG, "%s is not aligned", names[i]);
+    return hip_status(rhz::launch_prepare(*a, static_cast<hipStream_t>(stream)), "prepare launch");
+}
+
+rhz_status rhz_rmsnorm_heads(const rhz_rmsnorm_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->rows < 0) return fail(RHZ_ERR_INVALID_ARG, "rows must be >= 0 (got %d)", a->rows);
+    if (a->dim < 1) return fail(RHZ_ERR_INVALID_ARG, "dim must be >= 1 (got %d)", a->dim);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (a->dim > 1024) return fail(RHZ_ERR_UNSUPPORTED, "dim = %d exceeds the supported 1024", a->dim);
+    if (!(a->eps >= 0.f)) return fail(RHZ_ERR_INVALID_ARG, "eps must be >= 0");
+    if ((int64_t)a->rows * a->dim > kMaxIndex) return fail(RHZ_ERR_INVALID_ARG, "rows * dim exceeds 2^31 - 1");
+    if (a->rows == 0) return ok();
+    if (!a->x || !a->y || !a->scale) return fail(RHZ_ERR_INVALID_ARG, "x, y or scale is NULL");
+    const size_t ea = a->dtype == RHZ_F32 ? 4 : 2;
+    if (misaligned(a->x, ea) || misaligned(a->y, ea) || misaligned(a->scale, 4))
+        return fail(RHZ_ERR_INVALID_ARG, "x, y or scale is not aligned");
+    return hip_status(rhz::launch_rmsnorm(*a, static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
 rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count, int32_t row_len,
                            double mean, double std_dev, int32_t out_dtype, void* out, void* stream) {
     if (kind < RHZ_FILL_NORMAL || kind > RHZ_FILL_NEG_SOFTPLUS) return fail(RHZ_ERR_INVALID_ARG, "unknown kind %d", kind);

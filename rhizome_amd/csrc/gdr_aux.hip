@@ -1,0 +1,387 @@
+// gdr_aux.hip -- the Local-block steps on either side of the gated delta-rule
+// (SPEC.md:53-63), for gfx950.  All three are HBM-bound: each reads its
+// inputs once and writes its outputs once.
+//
+//   conv1d_kernel    causal depthwise conv1d of width 4 with a carried
+//                    3-sample state (causal_conv1d_step, delta.rs:232-243),
+//                    batched over packed sequences and channels;
+//   prepare_kernel   q, k L2-normalised (q rescaled), beta = sigmoid(logit),
+//                    g = -softplus(a_h) softplus(logit) (elementwise.rs:5-12,
+//                    36-42, 125-128);
+//   rmsnorm_kernel   RMSNorm of rows with a learned scale (norm.rs:8-13),
+//                    the per-head norm of the op's output (norm.rs:48-59).
+
+#include <type_traits>
+
+#include "gdr_device.hpp"
+#include "gdr_internal.hpp"
+
+namespace rhz {
+namespace {
+
+// N consecutive elements as floats: one 16-byte access when VEC (N = 4 fp32
+// or 8 bf16, 16-byte aligned), else N = 1.
+template <typename T, bool VEC>
+struct Vec {
+    static constexpr int N = VEC ? 16 / int(sizeof(T)) : 1;
+    // the loaded bits, unpacked later (4 registers for 16 bytes)
+    using Raw = typename std::conditional<VEC, uint4, T>::type;
+    static __device__ __forceinline__ Raw load_raw(const T* p) { return *reinterpret_cast<const Raw*>(p); }
+    static __device__ __forceinline__ void unpack(const Raw& r, float (&x)[N]) {
+        if constexpr (!VEC) {
+            x[0] = Elem<T>::load(&r, 0);
+        } else if constexpr (sizeof(T) == 4) {
+            x[0] = __uint_as_float(r.x); x[1] = __uint_as_float(r.y);
+            x[2] = __uint_as_float(r.z); x[3] = __uint_as_float(r.w);
+        } else {
+            const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[2 * i] = __uint_as_float(w[i] << 16);
+                x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
+        }
+    }
+    static __device__ __forceinline__ void load(const T* p, float (&x)[N]) { unpack(load_raw(p), x); }
+    static __device__ __forceinline__ void store(T* p, const float (&x)[N]) {
+        if constexpr (!VEC) {
+            Elem<T>::store(p, 0, x[0]);
+        } else if constexpr (sizeof(T) == 4) {
+            *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+        } else {
+            uint4 u;
+            u.x = pack_bf16x2(x[0], x[1]);
+            u.y = pack_bf16x2(x[2], x[3]);
+            u.z = pack_bf16x2(x[4], x[5]);
+            u.w = pack_bf16x2(x[6], x[7]);
+            *reinterpret_cast<uint4*>(p) = u;
+        }
+    }
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------- conv1d
+// Thread = (channel, span of kConvSpan consecutive tokens of the pack); a
+// span may cross sequence starts.  Each thread rebuilds its window of the
+// three previous inputs from x (or the sequence's initial state before its
+// start), so spans are independent and the grid covers tokens x channels.
+constexpr int kConvSpan = 16;
+
+struct ConvParams {
+    const void* x;
+    const float* w;
+    const float* bias;
+    const int* cu;
+    const float* init;
+    float* fin;
+    void* y;
+    int batch, seq_len, C;
+};
+
+// Sequence containing token t (packed: last s with cu[s] <= t; offsets are
+// clamped into [0, total]).
+__device__ __forceinline__ int seq_of(const ConvParams& p, int t) {
+    if (!p.cu) return t / max(p.seq_len, 1);
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (min(max(p.cu[mid], 0), p.seq_len) <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+__device__ __forceinline__ int seq_start(const ConvParams& p, int s) {
+    return p.cu ? min(max(p.cu[s], 0), p.seq_len) : s * p.seq_len;
+}
+__device__ __forceinline__ int seq_end(const ConvParams& p, int s) {
+    if (!p.cu) return (s + 1) * p.seq_len;
+    return min(max(p.cu[s + 1], seq_start(p, s)), p.seq_len);
+}
+
+// Grid: one dimension, block b = (span b / ncb, channel block b % ncb);
+// each thread owns N consecutive channels (one 16-byte access per token
+// when VEC).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, int ncb) {
+    using V = Vec<T, VEC>;
+    constexpr int N = V::N;
+    const int c = ((blockIdx.x % ncb) * 256 + threadIdx.x) * N;
+    const int t0 = (blockIdx.x / ncb) * kConvSpan;
+    if (c >= p.C || t0 >= total) return;
+    const int t1 = min(t0 + kConvSpan, total);
+    const T* __restrict__ x = static_cast<const T*>(p.x);  // y never overlaps x
+    T* __restrict__ y = static_cast<T*>(p.y);
+    const long C = p.C;
+    float w[N][4], b[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[e][j] = p.w[4 * (c + e) + j];
+        b[e] = p.bias ? p.bias[c + e] : 0.f;
+    }
+
+    int s = seq_of(p, t0);
+    int s0 = seq_start(p, s), s1 = seq_end(p, s);
+    // a[j][e]: input at position t - 3 + j of channel c + e (oldest first);
+    // before a sequence start the values come from its state, or are zero
+    float a[3][N];
+    auto window = [&](int seq, int start, int pos, float (&dst)[N]) {
+        if (pos >= start) {
+            V::load(x + pos * C + c, dst);
+        } else {
+            const int k = 3 + (pos - start);  // 0..2
+#pragma unroll
+            for (int e = 0; e < N; ++e) dst[e] = p.init ? p.init[((long)seq * C + c + e) * 3 + k] : 0.f;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < 3; ++j) window(s, s0, t0 - 3 + j, a[j]);
+    // every input of the span first, so that its loads overlap
+    typename V::Raw xs[kConvSpan];
+#pragma unroll
+    for (int i = 0; i < kConvSpan; ++i)
+        if (t0 + i < t1) xs[i] = V::load_raw(x + (t0 + i) * C + c);
+#pragma unroll
+    for (int i = 0; i < kConvSpan; ++i) {
+        const int t = t0 + i;
+        if (t >= t1) break;
+        while (t >= s1) {  // next sequence (skipping empty ones)
+            if (s + 1 >= p.batch) return;  // past the last sequence: not part of any
+            ++s;
+            s0 = seq_start(p, s);
+            s1 = seq_end(p, s);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) window(s, s0, s0 - 3 + j, a[j]);
+        }
+        float xt[N], yt[N];
+        V::unpack(xs[i], xt);
+#pragma unroll
+        for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
+            yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
+        V::store(y + t * C + c, yt);
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            a[0][e] = a[1][e];
+            a[1][e] = a[2][e];
+            a[2][e] = xt[e];
+        }
+        if (t == s1 - 1 && p.fin) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                float* f = p.fin + ((long)s * C + c + e) * 3;
+                f[0] = a[0][e];
+                f[1] = a[1][e];
+                f[2] = a[2][e];
+            }
+        }
+    }
+}
+
+// Final state of every empty sequence: its initial state (or zeros).
+// Grid: channel blocks x sequences (grid-stride over sequences).
+__global__ __launch_bounds__(256) void conv1d_empty_kernel(ConvParams p) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= p.C) return;
+    for (int s = blockIdx.y; s < p.batch; s += gridDim.y) {
+        if (seq_end(p, s) > seq_start(p, s)) continue;
+        const long o = ((long)s * p.C + c) * 3;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) p.fin[o + k] = p.init ? p.init[o + k] : 0.f;
+    }
+}
+
+// ---------------------------------------------------------------- prepare
+// A group of G lanes per (token, head) row; lane li holds elements li + G i.
+struct PrepParams {
+    const void* q_in;
+    const void* k_in;
+    void* q_out;
+    void* k_out;
+    const float* beta_logit;
+    const float* alpha_logit;
+    const float* a_log;
+    float* beta;
+    float* g;
+    int rows, heads, d;
+    float q_scale;
+};
+
+__device__ __forceinline__ float sigmoid_f(float x) {  // elementwise.rs:5-12
+    if (x >= 0.f) return 1.f / (1.f + expf(-x));
+    const float e = expf(x);
+    return e / (1.f + e);
+}
+__device__ __forceinline__ float softplus_f(float x) {  // elementwise.rs:36-42
+    return x > 30.f ? x : log1pf(expf(x));
+}
+
+// A row of d elements as vectors of N: lane li of the row's G lanes holds
+// vectors li + G i, i < NV (zero beyond the row).
+template <int G, int NV, typename T, bool VEC>
+struct RowSlice {
+    using V = Vec<T, VEC>;
+    static constexpr int N = V::N;
+    float v[NV][N];
+    __device__ __forceinline__ float load(const T* row, int d, int li) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = (li + G * i) * N;
+            if (j < d) {
+                V::load(row + j, v[i]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) v[i][e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < N; ++e) ss += v[i][e] * v[i][e];
+        }
+        return group_sum<G>(ss);
+    }
+    template <typename F>
+    __device__ __forceinline__ void store(T* row, int d, int li, F f) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = (li + G * i) * N;
+            if (j < d) {
+                float o[N];
+#pragma unroll
+                for (int e = 0; e < N; ++e) o[e] = f(j + e, v[i][e]);
+                V::store(row + j, o);
+            }
+        }
+    }
+};
+
+template <int G, int NV, typename T, bool VEC>
+__device__ __forceinline__ void l2norm_row(const T* in, T* out, int d, int li, float scale) {
+    RowSlice<G, NV, T, VEC> r;
+    const float ss = r.load(in, d, li);
+    const float f = scale / fmaxf(sqrtf(ss), 1e-12f);  // elementwise.rs:126-127
+    r.store(out, d, li, [&](int, float x) { return x * f; });
+}
+
+template <int G, int NV, typename T, bool VEC>
+__global__ __launch_bounds__(256) void prepare_kernel(PrepParams p) {
+    constexpr int RPB = 256 / G;
+    const int row = blockIdx.x * RPB + threadIdx.x / G;
+    const int li = threadIdx.x % G;
+    if (row >= p.rows) return;  // whole groups leave together (G divides 64)
+    const long base = (long)row * p.d;
+    l2norm_row<G, NV, T, VEC>(static_cast<const T*>(p.q_in) + base, static_cast<T*>(p.q_out) + base, p.d, li,
+                              p.q_scale);
+    l2norm_row<G, NV, T, VEC>(static_cast<const T*>(p.k_in) + base, static_cast<T*>(p.k_out) + base, p.d, li,
+                              1.f);
+    if (li == 0) {
+        const int h = row % p.heads;
+        p.beta[row] = sigmoid_f(p.beta_logit[row]);
+        p.g[row] = -softplus_f(p.a_log[h]) * softplus_f(p.alpha_logit[row]);
+    }
+}
+
+// ---------------------------------------------------------------- rmsnorm
+struct NormParams {
+    const void* x;
+    const float* scale;
+    void* y;
+    int rows, dim;
+    float eps;
+};
+
+template <int G, int NV, typename T, bool VEC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormParams p) {
+    constexpr int RPB = 256 / G;
+    const int row = blockIdx.x * RPB + threadIdx.x / G;
+    const int li = threadIdx.x % G;
+    if (row >= p.rows) return;
+    RowSlice<G, NV, T, VEC> r;
+    const float ss = r.load(static_cast<const T*>(p.x) + (long)row * p.dim, p.dim, li);
+    const float inv = 1.f / sqrtf(ss / (float)p.dim + p.eps);  // norm.rs:9-11
+    const float* scale = p.scale;
+    r.store(static_cast<T*>(p.y) + (long)row * p.dim, p.dim, li, [&](int j, float x) { return x * inv * scale[j]; });
+}
+
+// Rows of n elements: G lanes per row, NV vectors of N per lane (G NV N >= n).
+template <template <int, int, typename, bool> class K, int G, int NV, typename T, bool VEC, typename P>
+hipError_t go_rows(const P& p, int rows, hipStream_t st) {
+    constexpr int RPB = 256 / G;
+    hipLaunchKernelGGL((K<G, NV, T, VEC>::fn), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+template <int G, int NV, typename T, bool VEC>
+struct PrepK {
+    static constexpr auto fn = prepare_kernel<G, NV, T, VEC>;
+};
+template <int G, int NV, typename T, bool VEC>
+struct NormK {
+    static constexpr auto fn = rmsnorm_kernel<G, NV, T, VEC>;
+};
+// Vectors of 16 bytes when every row starts 16-byte aligned; the lanes per
+// row then cover n / N vectors.
+template <template <int, int, typename, bool> class K, typename T, typename P>
+hipError_t pick_rows(const P& p, int rows, int n, bool vec, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (vec) {
+        const int nv = n / (16 / int(sizeof(T)));  // vectors per row
+        if (nv <= 8) return go_rows<K, 8, 1, T, true>(p, rows, st);
+        if (nv <= 16) return go_rows<K, 16, 1, T, true>(p, rows, st);
+        if (nv <= 32) return go_rows<K, 32, 1, T, true>(p, rows, st);
+        if (nv <= 64) return go_rows<K, 64, 1, T, true>(p, rows, st);
+        if (nv <= 128) return go_rows<K, 64, 2, T, true>(p, rows, st);
+        return go_rows<K, 64, 4, T, true>(p, rows, st);  // n <= 1024 elements of 4 bytes
+    }
+    if (n <= 64) return go_rows<K, 16, 4, T, false>(p, rows, st);
+    if (n <= 128) return go_rows<K, 32, 4, T, false>(p, rows, st);
+    if (n <= 256) return go_rows<K, 32, 8, T, false>(p, rows, st);
+    if (n <= 512) return go_rows<K, 64, 8, T, false>(p, rows, st);
+    return go_rows<K, 64, 16, T, false>(p, rows, st);
+}
+
+}  // namespace
+
+hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t st) {
+    ConvParams p{a.x, a.weight, a.bias, a.cu_seqlens, a.initial_state, a.final_state, a.y,
+                 a.batch, a.seq_len, a.channels};
+    const int total = a.cu_seqlens ? a.seq_len : a.batch * a.seq_len;
+    const int es = a.dtype == RHZ_F32 ? 4 : 2, nvec = 16 / es;
+    const bool vec = a.channels % nvec == 0 && aligned16(a.x) && aligned16(a.y);
+    const int per_thread = vec ? nvec : 1;
+    const int ncb = (a.channels / per_thread + 255) / 256;
+    if (total > 0) {
+        const dim3 grid((unsigned)((long)ncb * ((total + kConvSpan - 1) / kConvSpan)));
+        if (a.dtype == RHZ_F32) {
+            if (vec) hipLaunchKernelGGL((conv1d_kernel<float, true>), grid, dim3(256), 0, st, p, total, ncb);
+            else hipLaunchKernelGGL((conv1d_kernel<float, false>), grid, dim3(256), 0, st, p, total, ncb);
+        } else {
+            if (vec) hipLaunchKernelGGL((conv1d_kernel<uint16_t, true>), grid, dim3(256), 0, st, p, total, ncb);
+            else hipLaunchKernelGGL((conv1d_kernel<uint16_t, false>), grid, dim3(256), 0, st, p, total, ncb);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (a.final_state) {
+        hipLaunchKernelGGL(conv1d_empty_kernel, dim3(ncb, min(a.batch, 65535)), dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_prepare(const rhz_gdr_prepare_args& a, hipStream_t st) {
+    PrepParams p{a.q_in, a.k_in, a.q_out, a.k_out, a.beta_logit, a.alpha_logit, a.a_log, a.beta, a.g,
+                 a.tokens * a.heads, a.heads, a.d_k, a.q_scale};
+    const int nvec = a.dtype == RHZ_F32 ? 4 : 8;
+    const bool vec = a.d_k % nvec == 0 && aligned16(a.q_in) && aligned16(a.k_in) && aligned16(a.q_out) &&
+                     aligned16(a.k_out);
+    if (a.dtype == RHZ_F32) return pick_rows<PrepK, float>(p, p.rows, a.d_k, vec, st);
+    return pick_rows<PrepK, uint16_t>(p, p.rows, a.d_k, vec, st);
+}
+
+hipError_t launch_rmsnorm(const rhz_rmsnorm_args& a, hipStream_t st) {
+    NormParams p{a.x, a.scale, a.y, a.rows, a.dim, a.eps};
+    const int nvec = a.dtype == RHZ_F32 ? 4 : 8;
+    const bool vec = a.dim % nvec == 0 && aligned16(a.x) && aligned16(a.y);
+    if (a.dtype == RHZ_F32) return pick_rows<NormK, float>(p, a.rows, a.dim, vec, st);
+    return pick_rows<NormK, uint16_t>(p, a.rows, a.dim, vec, st);
+}
+
+}  // namespace rhz

@@ -27,6 +27,11 @@ bool chunked_supported(int d_k, int d_v);
 size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a);
 hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream);
 
+// Local-block prologue and epilogue (gdr_aux.hip).
+hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t stream);
+hipError_t launch_prepare(const rhz_gdr_prepare_args& a, hipStream_t stream);
+hipError_t launch_rmsnorm(const rhz_rmsnorm_args& a, hipStream_t stream);
+
 // Device Philox-4x32-10 fill.
 hipError_t launch_philox_fill(int kind, uint64_t seed, uint64_t stream_id, int64_t count,
                               int row_len, double mean, double std_dev, int out_dtype, void* out,

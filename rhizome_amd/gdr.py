@@ -184,6 +184,69 @@ def multistep(q, k, v, g=None, beta=None, *, alpha=None, state, out=None, states
     return o, states
 
 
+def causal_conv1d(x, weight, bias=None, *, cu_seqlens=None, initial_state=None,
+                  output_final_state=False, out=None, stream=None):
+    """Causal depthwise conv1d of width 4 (delta.rs:232-243 per channel).
+
+    x [B, T, C] (dense) or [tokens, C] with ``cu_seqlens``; weight [C, 4]
+    fp32; bias [C]; initial_state [N, C, 3].  Returns (y, final_state or None).
+    """
+    if cu_seqlens is None:
+        B, T, C = x.shape
+        batch, seq_len = B, T
+    else:
+        seq_len, C = x.shape
+        batch = cu_seqlens.numel() - 1
+    if tuple(weight.shape) != (C, 4) or weight.dtype != torch.float32:
+        raise ValueError("weight must be fp32 [C, 4]")
+    y = out if out is not None else torch.empty_like(x)
+    fin = None
+    if output_final_state:
+        fin = torch.empty((batch, C, 3), dtype=torch.float32, device=x.device)
+    a = _abi.Conv1dArgs()
+    a.batch, a.seq_len, a.channels, a.dtype = batch, seq_len, C, _DTYPES[x.dtype]
+    a.x, a.weight, a.bias, a.y = _ptr(x), _ptr(weight), _ptr(bias), _ptr(y)
+    a.cu_seqlens, a.initial_state, a.final_state = _ptr(cu_seqlens), _ptr(initial_state), _ptr(fin)
+    _abi.check(_abi.lib().rhz_causal_conv1d(byref(a), _stream(stream)))
+    return y, fin
+
+
+def prepare(q, k, beta_logit, alpha_logit, a_log, *, q_scale=None, q_out=None, k_out=None,
+            stream=None):
+    """q := l2norm(q) * q_scale (default sqrt(d_k)), k := l2norm(k),
+    beta := sigmoid(beta_logit), g := -softplus(a_log[h]) * softplus(alpha_logit).
+
+    q, k [..., H, d_k]; logits [..., H]; a_log [H].  Returns (q, k, beta, g).
+    """
+    *lead, H, dk = q.shape
+    tokens = 1
+    for n in lead:
+        tokens *= n
+    qo = q_out if q_out is not None else torch.empty_like(q)
+    ko = k_out if k_out is not None else torch.empty_like(k)
+    beta = torch.empty(beta_logit.shape, dtype=torch.float32, device=q.device)
+    g = torch.empty_like(beta)
+    a = _abi.PrepareArgs()
+    a.tokens, a.heads, a.d_k, a.dtype = tokens, H, dk, _DTYPES[q.dtype]
+    a.q_scale = float(dk) ** 0.5 if q_scale is None else float(q_scale)
+    a.q_in, a.k_in, a.q_out, a.k_out = _ptr(q), _ptr(k), _ptr(qo), _ptr(ko)
+    a.beta_logit, a.alpha_logit, a.a_log = _ptr(beta_logit), _ptr(alpha_logit), _ptr(a_log)
+    a.beta, a.g = _ptr(beta), _ptr(g)
+    _abi.check(_abi.lib().rhz_gdr_prepare(byref(a), _stream(stream)))
+    return qo, ko, beta, g
+
+
+def rmsnorm_heads(x, scale, eps: float = 1e-6, *, out=None, stream=None):
+    """RMSNorm over the last dimension with a learned scale (norm.rs:8-13, 48-59)."""
+    dim = x.shape[-1]
+    y = out if out is not None else torch.empty_like(x)
+    a = _abi.RmsnormArgs()
+    a.rows, a.dim, a.dtype, a.eps = x.numel() // dim, dim, _DTYPES[x.dtype], eps
+    a.x, a.scale, a.y = _ptr(x), _ptr(scale), _ptr(y)
+    _abi.check(_abi.lib().rhz_rmsnorm_heads(byref(a), _stream(stream)))
+    return y
+
+
 _FILL = {"normal": _abi.FILL_NORMAL, "unit_rows": _abi.FILL_UNIT_ROWS,
          "sigmoid": _abi.FILL_SIGMOID, "neg_softplus": _abi.FILL_NEG_SOFTPLUS}
 _FILL_DTYPES = {torch.float64: _abi.F64, torch.float32: _abi.F32, torch.bfloat16: _abi.BF16}

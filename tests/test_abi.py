@@ -229,3 +229,67 @@ def test_python_front_end_rejects_host_tensors():
         rhizome_amd.prefill(q, q, q[..., :4, :], g, g)
     with pytest.raises(ValueError):
         rhizome_amd.prefill(q, q, q, g, g, alpha=g)
+
+
+def _conv(**over):
+    a = _abi.Conv1dArgs()
+    a.batch, a.seq_len, a.channels, a.dtype = 4, 4096, 2048, _abi.BF16
+    for name in ("x", "weight", "y"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(batch=0), "batch"), (dict(seq_len=-1), "seq_len"), (dict(channels=0), "channels"),
+    (dict(dtype=_abi.F64), "dtype"), (dict(x=None), "x or y is NULL"), (dict(weight=None), "weight"),
+    (dict(x=A + 1), "aligned"), (dict(bias=A + 2), "4-byte"), (dict(seq_len=1 << 20), "2^31"),
+])
+def test_conv1d_validation(over, msg):
+    assert _abi.lib().rhz_causal_conv1d(byref(_conv(**over)), None) == _abi.ERR_INVALID_ARG
+    assert msg in _abi.last_error()
+
+
+def _prep(**over):
+    a = _abi.PrepareArgs()
+    a.tokens, a.heads, a.d_k, a.dtype, a.q_scale = 16384, 16, 128, _abi.BF16, 11.3
+    for name in ("q_in", "k_in", "q_out", "k_out", "beta_logit", "alpha_logit", "a_log", "beta", "g"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(tokens=-1), _abi.ERR_INVALID_ARG, "tokens"), (dict(heads=0), _abi.ERR_INVALID_ARG, "heads"),
+    (dict(d_k=0), _abi.ERR_INVALID_ARG, "d_k"), (dict(dtype=3), _abi.ERR_INVALID_ARG, "dtype"),
+    (dict(d_k=257), _abi.ERR_UNSUPPORTED, "256"), (dict(a_log=None), _abi.ERR_INVALID_ARG, "a_log is NULL"),
+    (dict(g=A + 2), _abi.ERR_INVALID_ARG, "g is not aligned"),
+    (dict(tokens=1 << 20, heads=64), _abi.ERR_INVALID_ARG, "2^31"),
+])
+def test_prepare_validation(over, status, msg):
+    assert _abi.lib().rhz_gdr_prepare(byref(_prep(**over)), None) == status
+    assert msg in _abi.last_error()
+
+
+def test_prepare_and_rmsnorm_no_rows_is_ok():
+    assert _abi.lib().rhz_gdr_prepare(byref(_prep(tokens=0, q_in=None)), None) == _abi.OK
+    a = _abi.RmsnormArgs()
+    a.rows, a.dim, a.dtype, a.eps = 0, 128, _abi.F32, 1e-6
+    assert _abi.lib().rhz_rmsnorm_heads(byref(a), None) == _abi.OK
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(rows=-1), _abi.ERR_INVALID_ARG, "rows"), (dict(dim=0), _abi.ERR_INVALID_ARG, "dim"),
+    (dict(dim=1025), _abi.ERR_UNSUPPORTED, "1024"), (dict(eps=-1.0), _abi.ERR_INVALID_ARG, "eps"),
+    (dict(scale=None), _abi.ERR_INVALID_ARG, "NULL"), (dict(dtype=_abi.F64), _abi.ERR_INVALID_ARG, "dtype"),
+])
+def test_rmsnorm_validation(over, status, msg):
+    a = _abi.RmsnormArgs()
+    a.rows, a.dim, a.dtype, a.eps = 16384 * 16, 128, _abi.BF16, 1e-6
+    a.x, a.scale, a.y = A, A, A
+    for key, val in over.items():
+        setattr(a, key, val)
+    assert _abi.lib().rhz_rmsnorm_heads(byref(a), None) == status
+    assert msg in _abi.last_error()

@@ -1,0 +1,108 @@
+"""GPU parity of the Local-block prologue and epilogue around the op against
+the f64 oracle, through the C ABI:
+  rhz_causal_conv1d   causal_conv1d_step (crates/ops/src/delta.rs:232-243) along
+                      packed sequences, carried state, reset at sequence starts
+  rhz_gdr_prepare     l2norm / sigmoid / softplus (elementwise.rs:5-12, 36-42, 125-128)
+                      composed as SPEC.md:53-56 describes
+  rhz_rmsnorm_heads   rmsnorm / groupnorm_heads (norm.rs:8-13, 48-59)
+"""
+import numpy as np
+import pytest
+import torch
+
+import rhizome_amd
+from gdr_cases import BF16_TOL, F32_TOL, check_close, to_device
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+PATHS = [(torch.float32, F32_TOL), (torch.bfloat16, BF16_TOL)]
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+@pytest.mark.parametrize("dtype,tol", PATHS)
+@pytest.mark.parametrize("lengths,C,with_state", [
+    ([100, 100], 300, False),             # dense-shaped pack
+    ([0, 1, 2, 3, 31, 32, 33, 0, 200], 257, True),   # empty and short sequences, span edges
+    ([4096], 2048, True),
+])
+def test_conv1d(device, dtype, tol, lengths, C, with_state):
+    rng = _rng(len(lengths) + C)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    x, x64 = to_device(rng.normal(size=(cu[-1], C)), dtype, device)
+    w, w64 = to_device(rng.normal(scale=0.5, size=(C, 4)), torch.float32, device)
+    b, b64 = to_device(rng.normal(size=C), torch.float32, device)
+    init = init64 = None
+    if with_state:
+        init, init64 = to_device(rng.normal(size=(len(lengths), C, 3)), torch.float32, device)
+    cu_dev = torch.from_numpy(cu.astype(np.int32)).to(device)
+    y, fin = rhizome_amd.causal_conv1d(x, w, b, cu_seqlens=cu_dev, initial_state=init,
+                                       output_final_state=True)
+    torch.cuda.synchronize()
+    ry, rf = O.conv1d_batched(cu, x64, w64, b64, init64)
+    my = check_close(y.float().cpu().numpy(), ry, tol, f"conv1d y {dtype}")
+    mf = check_close(fin.cpu().numpy(), rf, tol, f"conv1d final state {dtype}")
+    print(f"conv1d {lengths[:4]}.. C={C} {dtype}: y {my} final {mf}", flush=True)
+
+
+def test_conv1d_dense_equals_packed(device):
+    rng = _rng(9)
+    B, T, C = 3, 77, 64
+    x = torch.from_numpy(rng.normal(size=(B, T, C)).astype(np.float32)).to(device)
+    w = torch.from_numpy(rng.normal(size=(C, 4)).astype(np.float32)).to(device)
+    y1, f1 = rhizome_amd.causal_conv1d(x, w, output_final_state=True)
+    cu = torch.arange(0, B * T + 1, T, dtype=torch.int32, device=device)
+    y2, f2 = rhizome_amd.causal_conv1d(x.reshape(B * T, C), w, cu_seqlens=cu, output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.reshape(B * T, C), y2) and torch.equal(f1, f2)
+
+
+@pytest.mark.parametrize("dtype,tol", PATHS)
+@pytest.mark.parametrize("tokens,H,dk", [(1000, 4, 128), (5, 3, 64), (37, 2, 256), (64, 3, 37)])
+def test_prepare(device, dtype, tol, tokens, H, dk):
+    rng = _rng(tokens + dk)
+    q, q64 = to_device(rng.normal(size=(tokens, H, dk)), dtype, device)
+    k, k64 = to_device(rng.normal(size=(tokens, H, dk)), dtype, device)
+    bl, bl64 = to_device(rng.normal(scale=3, size=(tokens, H)), torch.float32, device)
+    al, al64 = to_device(rng.normal(scale=3, size=(tokens, H)), torch.float32, device)
+    a, a64 = to_device(rng.normal(size=H), torch.float32, device)
+    qo, ko, beta, g = rhizome_amd.prepare(q, k, bl, al, a)
+    torch.cuda.synchronize()
+    rq, rk, rb, rg = O.prepare(q64, k64, bl64, al64, a64, float(dk) ** 0.5)
+    m = [check_close(qo.float().cpu().numpy(), rq, tol, "q"), check_close(ko.float().cpu().numpy(), rk, tol, "k"),
+         check_close(beta.cpu().numpy(), rb, F32_TOL, "beta"), check_close(g.cpu().numpy(), rg, F32_TOL, "g")]
+    print(f"prepare {tokens}x{H}x{dk} {dtype}: {m}", flush=True)
+
+
+def test_prepare_in_place(device):
+    rng = _rng(2)
+    q = torch.from_numpy(rng.normal(size=(50, 4, 128)).astype(np.float32)).to(device)
+    k = torch.from_numpy(rng.normal(size=(50, 4, 128)).astype(np.float32)).to(device)
+    z = torch.zeros((50, 4), device=device)
+    a = torch.zeros(4, device=device)
+    q1, k1, _, _ = rhizome_amd.prepare(q, k, z, z, a)
+    q2, k2, _, _ = rhizome_amd.prepare(q, k, z, z, a, q_out=q, k_out=k)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(k1, k2)
+    assert torch.allclose(k2.norm(dim=-1), torch.ones(50, 4, device=device), rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,tol", PATHS)
+@pytest.mark.parametrize("rows,dim", [(2000, 128), (33, 100), (7, 1024), (300, 64), (9, 1)])
+def test_rmsnorm(device, dtype, tol, rows, dim):
+    rng = _rng(rows + dim)
+    x, x64 = to_device(rng.normal(scale=3, size=(rows, dim)), dtype, device)
+    s, s64 = to_device(rng.normal(size=dim), torch.float32, device)
+    y = rhizome_amd.rmsnorm_heads(x, s, 1e-6)
+    torch.cuda.synchronize()
+    m = check_close(y.float().cpu().numpy(), O.rmsnorm_rows(x64, s64, 1e-6), tol, "rmsnorm")
+    print(f"rmsnorm {rows}x{dim} {dtype}: {m}", flush=True)
+
+
+def test_rmsnorm_in_place_and_heads_independent(device):
+    x = torch.tensor([[1.0, 1.0], [100.0, 100.0]], device=device)  # norm.rs:117-123
+    y = rhizome_amd.rmsnorm_heads(x, torch.ones(2, device=device), 1e-12, out=x)
+    torch.cuda.synchronize()
+    assert abs(float(y[0, 0]) - float(y[1, 0])) < 1e-6 and y.data_ptr() == x.data_ptr()

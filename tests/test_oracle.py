@@ -314,3 +314,72 @@ def test_golden_config0():
     with open(os.path.join(HERE, "golden", "config0.json")) as f:
         gold = json.load(f)
     assert config0_digest() == gold
+
+
+# ------------------------------------------------- prologue / epilogue pins
+def test_conv1d_batched_matches_reference_kat_and_step():
+    # delta.rs:360-369: w = [0.1, 0.2, 0.3, 0.4], x = 1 -> 0.4, 0.7; state [0, 1, 1]
+    y, fin = O.conv1d_batched([0, 2], np.ones((2, 1)), np.array([[0.1, 0.2, 0.3, 0.4]]))
+    assert abs(y[0, 0] - 0.4) < 1e-12 and abs(y[1, 0] - 0.7) < 1e-12
+    assert np.array_equal(fin[0, 0], [0.0, 1.0, 1.0])
+
+
+def test_conv1d_batched_against_dense_convolution():
+    """Brute force: each sequence and channel is a full convolution of
+    (initial state ++ x) with the reversed weights."""
+    rng = np.random.default_rng(3)
+    C = 5
+    cu = np.array([0, 7, 7, 8, 20])
+    x = rng.normal(size=(cu[-1], C))
+    w = rng.normal(size=(C, 4))
+    b = rng.normal(size=C)
+    init = rng.normal(size=(4, C, 3))
+    y, fin = O.conv1d_batched(cu, x, w, b, init)
+    for s in range(4):
+        for c in range(C):
+            seq = np.concatenate([init[s, c], x[cu[s]:cu[s + 1], c]])
+            for t in range(cu[s], cu[s + 1]):
+                i = t - cu[s] + 3
+                ref = seq[i - 3] * w[c, 0] + seq[i - 2] * w[c, 1] + seq[i - 1] * w[c, 2] + seq[i] * w[c, 3] + b[c]
+                assert abs(y[t, c] - ref) < 1e-12
+            assert np.allclose(fin[s, c], seq[-3:], rtol=0, atol=0)
+
+
+def test_conv1d_shift_and_identity_weights():
+    x = np.arange(1.0, 11.0).reshape(10, 1)
+    y, _ = O.conv1d_batched([0, 4, 10], x, np.array([[0.0, 0.0, 1.0, 0.0]]))  # y_t = x_{t-1}
+    assert np.array_equal(y[:, 0], [0, 1, 2, 3, 0, 5, 6, 7, 8, 9])  # reset at the second start
+    y, _ = O.conv1d_batched([0, 10], x, np.array([[0.0, 0.0, 0.0, 1.0]]), np.array([0.5]))
+    assert np.array_equal(y[:, 0], x[:, 0] + 0.5)
+
+
+def test_rmsnorm_rows():
+    # norm.rs:117-123: heads are normalised independently
+    y = O.rmsnorm_rows(np.array([[1.0, 1.0], [100.0, 100.0]]), np.ones(2), 1e-12)
+    assert abs(y[0, 0] - y[1, 0]) < 1e-6
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(6, 9))
+    s = rng.normal(size=9)
+    y = O.rmsnorm_rows(x, s, 0.0)
+    assert np.allclose(O.rmsnorm_rows(3.7 * x, s, 0.0), y, rtol=1e-13, atol=0)  # scale invariant
+    assert np.allclose(np.sqrt(np.mean((y / s) ** 2, axis=1)), 1.0, rtol=1e-13)  # unit RMS
+    assert np.allclose(O.rmsnorm_rows(np.full((1, 4), -2.0), np.arange(1.0, 5.0), 0.0), -np.arange(1.0, 5.0))
+
+
+def test_prepare():
+    q, k, beta, g = O.prepare(np.array([[[3.0, 4.0]]]), np.array([[[0.0, -5.0]]]),
+                              np.array([[0.0]]), np.array([[0.0]]), np.array([0.0]), 2.0)
+    assert np.allclose(q, [[[1.2, 1.6]]], rtol=0, atol=1e-15)  # elementwise.rs:224-227
+    assert np.allclose(k, [[[0.0, -1.0]]], rtol=0, atol=1e-15)
+    assert beta[0, 0] == 0.5
+    assert abs(g[0, 0] + np.log(2.0) ** 2) < 1e-15
+    rng = np.random.default_rng(5)
+    z = rng.normal(scale=4, size=(7, 3))
+    a = rng.normal(size=3)
+    _, _, beta, g = O.prepare(np.ones((7, 3, 2)), np.ones((7, 3, 2)), z, z, a, 1.0)
+    assert np.allclose(beta, 1 / (1 + np.exp(-z)), rtol=1e-14)
+    assert np.allclose(g, -np.log1p(np.exp(a))[None, :] * np.log1p(np.exp(z)), rtol=1e-12)
+    _, _, b2, g2 = O.prepare(np.ones((1, 1, 2)), np.ones((1, 1, 2)), np.array([[-1000.0]]),
+                             np.array([[40.0]]), np.array([35.0]), 1.0)
+    assert 0.0 <= b2[0, 0] < 1e-300  # elementwise.rs:151-153
+    assert g2[0, 0] == -35.0 * 40.0  # softplus is linear above 30
