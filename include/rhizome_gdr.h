@@ -99,7 +99,8 @@ typedef struct rhz_gdr_prefill_args {
                                    decreasing offsets give unspecified (memory-safe)
                                    results. */
     const float* initial_state; /* device [batch, H, d_v, d_k], or NULL for zeros */
-    float* final_state;         /* device [batch, H, d_v, d_k], or NULL */
+    float* final_state;         /* device [batch, H, d_v, d_k], or NULL; may equal
+                                   initial_state (the state is then updated in place) */
     void* o;                    /* device [tokens, H, d_v], dtype */
     void* workspace;            /* device scratch, 256-byte aligned */
     size_t workspace_bytes;

@@ -28,18 +28,10 @@
 #include <utility>
 #include <vector>
 
+#include "rhizome_error.hpp"
+
 namespace rhizome {
 namespace ops {
-
-class Error : public std::runtime_error {
-public:
-    Error(int32_t status, const std::string& what) : std::runtime_error(what), status_(status) {}
-    // An rhz_status of include/rhizome_gdr.h (RHZ_ERR_INVALID_ARG for a shape error).
-    int32_t status() const { return status_; }
-
-private:
-    int32_t status_;
-};
 
 // Per-position inputs for one head (delta.rs:12-29): rows T x head_dim,
 // alpha in (0, 1], beta in (0, 1), and a segment id per position (a change
