@@ -733,7 +733,8 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
 }
 
 // Loader wave LW, chunk x (buffer B = x & 1): stage x from registers, load
-// x + 1, then Q K^T of x.
+// x + 2 into the same registers, then Q K^T of x.  Each register set has
+// two chunk periods to arrive.
 template <int DK, int B, int LW>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
@@ -744,7 +745,7 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
     stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
     signal(&sm.sync.staged);
-    if (x + 1 < u.nch) load_chunk_any<DK>(p, u, x + 1, lo, lt, in);
+    if (x + 2 < u.nch) load_chunk_any<DK>(p, u, x + 2, lo, lt, in);
     wait_ge(&sm.sync.staged, 4 * (x + 1));
     qk_blocks<DK, B, LW>(sm, lt & 63);
     signal(&sm.sync.pdone);
@@ -754,11 +755,12 @@ template <int DK, int LW>
 __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int lt) {
     LoadOffsets<DK> lo;
     lo.set(p, u.i0, lt, kChunk - 1);
-    ChunkIn<DK> in;
-    if (u.nch > 0) load_chunk_any<DK>(p, u, 0, lo, lt, in);
+    ChunkIn<DK> in0, in1;
+    if (u.nch > 0) load_chunk_any<DK>(p, u, 0, lo, lt, in0);
+    if (u.nch > 1) load_chunk_any<DK>(p, u, 1, lo, lt, in1);
     for (int x = 0; x < u.nch; x += 2) {
-        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, in);
-        if (x + 1 < u.nch) prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, in);
+        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, in0);
+        if (x + 1 < u.nch) prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, in1);
     }
 }
 
