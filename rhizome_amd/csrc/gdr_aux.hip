@@ -59,7 +59,7 @@ struct Vec {
     }
 };
 
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---------------------------------------------------------------- conv1d
 // Thread = (channel, span of kConvSpan consecutive tokens of the pack); a
@@ -113,15 +113,64 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
     T* __restrict__ y = static_cast<T*>(p.y);
     const long C = p.C;
     float w[N][4], b[N];
+    if (aligned16(p.w)) {  // uniform: one 16-byte load per channel
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
+        for (int e = 0; e < N; ++e) {
+            const float4 f = reinterpret_cast<const float4*>(p.w)[c + e];
+            w[e][0] = f.x;
+            w[e][1] = f.y;
+            w[e][2] = f.z;
+            w[e][3] = f.w;
+        }
+    } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[e][j] = p.w[4 * (c + e) + j];
-        b[e] = p.bias ? p.bias[c + e] : 0.f;
+        for (int e = 0; e < N; ++e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[e][j] = p.w[4 * (c + e) + j];
     }
+#pragma unroll
+    for (int e = 0; e < N; ++e) b[e] = p.bias ? p.bias[c + e] : 0.f;
 
     int s = seq_of(p, t0);
     int s0 = seq_start(p, s), s1 = seq_end(p, s);
+    if (t1 - t0 == kConvSpan && t0 - 3 >= s0 && t1 <= s1) {
+        // A whole span inside one sequence, three tokens or more past its
+        // start: the window comes from x and no state is reset or read, so
+        // the span is straight-line code with every load issued up front.
+        float a[3][N];
+        typename V::Raw ws[3], xs[kConvSpan];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) ws[j] = V::load_raw(x + (t0 - 3 + j) * C + c);
+#pragma unroll
+        for (int i = 0; i < kConvSpan; ++i) xs[i] = V::load_raw(x + (t0 + i) * C + c);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) V::unpack(ws[j], a[j]);
+#pragma unroll
+        for (int i = 0; i < kConvSpan; ++i) {
+            float xt[N], yt[N];
+            V::unpack(xs[i], xt);
+#pragma unroll
+            for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
+                yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
+            V::store(y + (t0 + i) * C + c, yt);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                a[0][e] = a[1][e];
+                a[1][e] = a[2][e];
+                a[2][e] = xt[e];
+            }
+        }
+        if (t1 == s1 && p.fin) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                float* f = p.fin + ((long)s * C + c + e) * 3;
+                f[0] = a[0][e];
+                f[1] = a[1][e];
+                f[2] = a[2][e];
+            }
+        }
+        return;
+    }
     // a[j][e]: input at position t - 3 + j of channel c + e (oldest first);
     // before a sequence start the values come from its state, or are zero
     float a[3][N];
