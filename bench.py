@@ -233,10 +233,10 @@ def bench_aux(torch, steps, warmup):
         "conv1d": (lambda: rhizome_amd.causal_conv1d(x.view(1, T, C), w, cb, out=y.view(1, T, C)),
                    2 * T * C * 2 + C * 20, "conv1d_kernel<bf16>", "B=1 T=16384, 6144 channels"),
         "prepare": (lambda: rhizome_amd.prepare(q, k, lg, lg, a, q_out=qo, k_out=ko),
-                    4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<32,4,bf16>",
+                    4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<16,1,bf16,vec>",
                     "16384 tokens, H=16, d_k=128"),
         "rmsnorm": (lambda: rhizome_amd.rmsnorm_heads(o, sc, 1e-6, out=on), 2 * T * H * d * 2 + d * 4,
-                    "rmsnorm_kernel<32,4,bf16>", "16384 x 16 rows of 128"),
+                    "rmsnorm_kernel<16,1,bf16,vec>", "16384 x 16 rows of 128"),
     }
     out = {}
     for name, (fn, nbytes, kernel, shape) in jobs.items():

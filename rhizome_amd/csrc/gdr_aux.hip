@@ -271,13 +271,23 @@ struct RowSlice {
     using V = Vec<T, VEC>;
     static constexpr int N = V::N;
     float v[NV][N];
-    __device__ __forceinline__ float load(const T* row, int d, int li) {
+    typename V::Raw raw[NV];
+    // issue() starts the loads, reduce() unpacks them and returns the row's
+    // sum of squares; rows whose loads are all issued first overlap them.
+    __device__ __forceinline__ void issue(const T* row, int d, int li) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = (li + G * i) * N;
+            if (j < d) raw[i] = V::load_raw(row + j);
+        }
+    }
+    __device__ __forceinline__ float reduce(int d, int li) {
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int j = (li + G * i) * N;
             if (j < d) {
-                V::load(row + j, v[i]);
+                V::unpack(raw[i], v[i]);
             } else {
 #pragma unroll
                 for (int e = 0; e < N; ++e) v[i][e] = 0.f;
@@ -286,6 +296,10 @@ struct RowSlice {
             for (int e = 0; e < N; ++e) ss += v[i][e] * v[i][e];
         }
         return group_sum<G>(ss);
+    }
+    __device__ __forceinline__ float load(const T* row, int d, int li) {
+        issue(row, d, li);
+        return reduce(d, li);
     }
     template <typename F>
     __device__ __forceinline__ void store(T* row, int d, int li, F f) {
@@ -302,29 +316,43 @@ struct RowSlice {
     }
 };
 
-template <int G, int NV, typename T, bool VEC>
-__device__ __forceinline__ void l2norm_row(const T* in, T* out, int d, int li, float scale) {
-    RowSlice<G, NV, T, VEC> r;
-    const float ss = r.load(in, d, li);
-    const float f = scale / fmaxf(sqrtf(ss), 1e-12f);  // elementwise.rs:126-127
-    r.store(out, d, li, [&](int, float x) { return x * f; });
-}
-
+// q and k of a (token, head) row L2-normalised (elementwise.rs:126-127: x /
+// max(|x|, 1e-12) * scale), and its gates.  Every load of the row is issued
+// before the first store, which also makes q_out = q_in and k_out = k_in safe.
+// A group of G lanes handles rows r and r + RPB of its block's 2 RPB rows.
 template <int G, int NV, typename T, bool VEC>
 __global__ __launch_bounds__(256) void prepare_kernel(PrepParams p) {
     constexpr int RPB = 256 / G;
-    const int row = blockIdx.x * RPB + threadIdx.x / G;
+    const int row0 = blockIdx.x * 2 * RPB + threadIdx.x / G;
     const int li = threadIdx.x % G;
-    if (row >= p.rows) return;  // whole groups leave together (G divides 64)
-    const long base = (long)row * p.d;
-    l2norm_row<G, NV, T, VEC>(static_cast<const T*>(p.q_in) + base, static_cast<T*>(p.q_out) + base, p.d, li,
-                              p.q_scale);
-    l2norm_row<G, NV, T, VEC>(static_cast<const T*>(p.k_in) + base, static_cast<T*>(p.k_out) + base, p.d, li,
-                              1.f);
-    if (li == 0) {
-        const int h = row % p.heads;
-        p.beta[row] = sigmoid_f(p.beta_logit[row]);
-        p.g[row] = -softplus_f(p.a_log[h]) * softplus_f(p.alpha_logit[row]);
+    RowSlice<G, NV, T, VEC> rq[2], rk[2];
+    float bl[2] = {0.f, 0.f}, al[2] = {0.f, 0.f}, ah[2] = {0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int row = row0 + u * RPB;
+        if (row >= p.rows) break;  // uniform over the group (G divides 64)
+        const long base = (long)row * p.d;
+        rq[u].issue(static_cast<const T*>(p.q_in) + base, p.d, li);
+        rk[u].issue(static_cast<const T*>(p.k_in) + base, p.d, li);
+        if (li == 0) {
+            bl[u] = p.beta_logit[row];
+            al[u] = p.alpha_logit[row];
+            ah[u] = p.a_log[row % p.heads];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int row = row0 + u * RPB;
+        if (row >= p.rows) break;
+        const long base = (long)row * p.d;
+        const float fq = p.q_scale / fmaxf(sqrtf(rq[u].reduce(p.d, li)), 1e-12f);
+        const float fk = 1.f / fmaxf(sqrtf(rk[u].reduce(p.d, li)), 1e-12f);
+        rq[u].store(static_cast<T*>(p.q_out) + base, p.d, li, [&](int, float x) { return x * fq; });
+        rk[u].store(static_cast<T*>(p.k_out) + base, p.d, li, [&](int, float x) { return x * fk; });
+        if (li == 0) {
+            p.beta[row] = sigmoid_f(bl[u]);
+            p.g[row] = -softplus_f(ah[u]) * softplus_f(al[u]);
+        }
     }
 }
 
@@ -337,24 +365,35 @@ struct NormParams {
     float eps;
 };
 
+// A group of G lanes handles rows r and r + RPB of its block's 2 RPB rows.
 template <int G, int NV, typename T, bool VEC>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormParams p) {
     constexpr int RPB = 256 / G;
-    const int row = blockIdx.x * RPB + threadIdx.x / G;
+    const int row0 = blockIdx.x * 2 * RPB + threadIdx.x / G;
     const int li = threadIdx.x % G;
-    if (row >= p.rows) return;
-    RowSlice<G, NV, T, VEC> r;
-    const float ss = r.load(static_cast<const T*>(p.x) + (long)row * p.dim, p.dim, li);
-    const float inv = 1.f / sqrtf(ss / (float)p.dim + p.eps);  // norm.rs:9-11
+    RowSlice<G, NV, T, VEC> r[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int row = row0 + u * RPB;
+        if (row >= p.rows) break;  // uniform over the group
+        r[u].issue(static_cast<const T*>(p.x) + (long)row * p.dim, p.dim, li);
+    }
     const float* scale = p.scale;
-    r.store(static_cast<T*>(p.y) + (long)row * p.dim, p.dim, li, [&](int j, float x) { return x * inv * scale[j]; });
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int row = row0 + u * RPB;
+        if (row >= p.rows) break;
+        const float inv = 1.f / sqrtf(r[u].reduce(p.dim, li) / (float)p.dim + p.eps);  // norm.rs:9-11
+        r[u].store(static_cast<T*>(p.y) + (long)row * p.dim, p.dim, li,
+                   [&](int j, float x) { return x * inv * scale[j]; });
+    }
 }
 
 // Rows of n elements: G lanes per row, NV vectors of N per lane (G NV N >= n).
 template <template <int, int, typename, bool> class K, int G, int NV, typename T, bool VEC, typename P>
 hipError_t go_rows(const P& p, int rows, hipStream_t st) {
-    constexpr int RPB = 256 / G;
-    hipLaunchKernelGGL((K<G, NV, T, VEC>::fn), dim3((rows + RPB - 1) / RPB), dim3(256), 0, st, p);
+    constexpr int RPB = 256 / G;  // rows per block and pass; each block takes two passes
+    hipLaunchKernelGGL((K<G, NV, T, VEC>::fn), dim3((rows + 2 * RPB - 1) / (2 * RPB)), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 template <int G, int NV, typename T, bool VEC>
