@@ -312,19 +312,26 @@ __device__ __forceinline__ void signal(int* cnt) {
     asm volatile("" ::: "memory");
 }
 // Waits until every counter c[i] >= t[i] (a target <= 0 holds at once).
-// Each poll reads all N counters back to back, so a wait costs one LDS
-// round trip however many counters it checks; polls follow each other
-// without sleeping (measured faster than s_sleep between polls).
+// Lane i < N polls counter i against t[i] (the other lanes always pass), so
+// a poll is one LDS read and one compare however many counters it checks,
+// and a waiting wave takes few issue slots from the wave beside it on its
+// SIMD.  Polls follow each other without sleeping (measured faster than
+// s_sleep between polls).
+typedef __attribute__((address_space(3))) int lds_int;
 template <int N>
 __device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) {
+    const int lane = __lane_id();
+    const lds_int* addr = (const lds_int*)c[0];
+    int tgt = -0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (lane == i) {
+            addr = (const lds_int*)c[i];
+            tgt = t[i];
+        }
     for (int spin = 0; spin < kSpinLimit; ++spin) {
-        int v[N];
-#pragma unroll
-        for (int i = 0; i < N; ++i) v[i] = __hip_atomic_load(c[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < N; ++i) ok &= __builtin_amdgcn_readfirstlane(v[i]) >= t[i];
-        if (ok) break;
+        const int v = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__builtin_amdgcn_ballot_w64(v < tgt) == 0) break;
     }
     asm volatile("" ::: "memory");
 }
