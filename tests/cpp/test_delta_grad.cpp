@@ -329,6 +329,68 @@ void batched_threads_agree() {  // the thread count does not change a bit
     for (int i = 0; i < 5; ++i) EXPECT(out[0][i] == out[1][i]);
 }
 
+// The batched form on a dense batch with zero initial states, head by head,
+// equals the one-head form (which resets at t = 0), bit for bit: the same
+// reverse scan over strided rows.
+void batched_equals_one_head() {
+    const std::size_t B = 2, T = 130, H = 3, d = 8, rows = B * T * H;
+    std::vector<double> q = normal(3, 1, rows * d), k = normal(3, 2, rows * d);
+    orc_l2norm_rows(q.data(), rows, d, 1.0, 1);
+    orc_l2norm_rows(k.data(), rows, d, 1.0, 1);
+    const std::vector<double> v = normal(3, 3, rows * d), wo = normal(3, 40, rows * d), wf = normal(3, 41, B * H * d * d);
+    std::vector<double> alpha(rows), beta(rows);
+    const std::vector<double> za = normal(3, 5, rows), zb = normal(3, 4, rows);
+    orc_sigmoid_vec(zb.data(), rows, beta.data());
+    orc_sigmoid_vec(za.data(), rows, alpha.data());
+    std::vector<double> dq(rows * d), dk(rows * d), dv(rows * d), da(rows), db(rows);
+    PrefillBackwardArgs a;
+    a.batch = B;
+    a.seq_len = T;
+    a.heads = H;
+    a.d_k = a.d_v = d;
+    a.gate_kind = RHZ_GATE_ALPHA;
+    a.q = q.data();
+    a.k = k.data();
+    a.v = v.data();
+    a.gate = alpha.data();
+    a.beta = beta.data();
+    a.d_o = wo.data();
+    a.d_final_state = wf.data();
+    a.dq = dq.data();
+    a.dk = dk.data();
+    a.dv = dv.data();
+    a.dgate = da.data();
+    a.dbeta = db.data();
+    a.threads = 4;
+    gated_delta_prefill_backward(a);
+    for (std::size_t b = 0; b < B; ++b)
+        for (std::size_t h = 0; h < H; ++h) {
+            DeltaInputs in;
+            in.head_dim = d;
+            std::vector<double> w_o(T * d);
+            for (std::size_t t = 0; t < T; ++t) {
+                const std::size_t r = (b * T + t) * H + h;
+                in.q.insert(in.q.end(), q.begin() + r * d, q.begin() + (r + 1) * d);
+                in.k.insert(in.k.end(), k.begin() + r * d, k.begin() + (r + 1) * d);
+                in.v.insert(in.v.end(), v.begin() + r * d, v.begin() + (r + 1) * d);
+                in.alpha.push_back(alpha[r]);
+                in.beta.push_back(beta[r]);
+                in.segment.push_back(0);
+                std::copy(wo.begin() + r * d, wo.begin() + (r + 1) * d, w_o.begin() + t * d);
+            }
+            DeltaState dfin;
+            dfin.head_dim = d;
+            dfin.s.assign(wf.begin() + (b * H + h) * d * d, wf.begin() + (b * H + h + 1) * d * d);
+            const DeltaGrads g = gated_delta_sequential_backward(in, DeltaState::zeros(d), w_o, &dfin);
+            for (std::size_t t = 0; t < T; ++t) {
+                const std::size_t r = (b * T + t) * H + h;
+                EXPECT(g.alpha[t] == da[r] && g.beta[t] == db[r]);
+                for (std::size_t j = 0; j < d; ++j)
+                    EXPECT(g.q[t * d + j] == dq[r * d + j] && g.k[t * d + j] == dk[r * d + j] && g.v[t * d + j] == dv[r * d + j]);
+            }
+        }
+}
+
 }  // namespace
 
 int main() {
@@ -344,6 +406,7 @@ int main() {
     run("batched_packed_alpha_gate", [] { batched_packed(RHZ_GATE_ALPHA); });
     run("batched_log_gate_is_chain_rule", batched_log_gate_is_chain_rule);
     run("batched_threads_agree", batched_threads_agree);
+    run("batched_equals_one_head", batched_equals_one_head);
     std::printf("OK: %d failed\n", g_failed);
     return g_failed ? 1 : 0;
 }

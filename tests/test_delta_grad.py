@@ -20,6 +20,6 @@ def test_adjoint_gradcheck():
     assert res.returncode == 0, res.stdout + res.stderr
     for name in ("sequential_single_segment", "sequential_with_segments", "sequential_across_windows",
                  "linear_in_v_and_q", "reset_cuts_gradients", "batched_packed_alpha_gate",
-                 "batched_log_gate_is_chain_rule", "batched_threads_agree"):
+                 "batched_log_gate_is_chain_rule", "batched_threads_agree", "batched_equals_one_head"):
         assert f"PASS {name}" in res.stdout
     assert "OK: 0 failed" in res.stdout
