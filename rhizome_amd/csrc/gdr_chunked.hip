@@ -31,7 +31,8 @@
 // The other six waves prepare the state-independent data of the next chunk
 // into the other half of double-buffered LDS:
 //   waves 4-7 (loaders): K, Q, beta V and the gates of chunk c into LDS from
-//               registers, chunk c+1 into registers, then Q K^T of chunk c;
+//               registers, chunk c+2 into the same registers (two register
+//               sets alternate), then Q K^T of chunk c;
 //   wave 2:     K K^T's diagonal blocks, T's diagonal blocks by forward
 //               substitution, T's blocks (1,0), (2,0), (3,0);
 //   wave 3:     K K^T below the diagonal, T's blocks (3,2), (2,1), (3,1).
