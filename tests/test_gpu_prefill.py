@@ -140,3 +140,22 @@ def test_config4_varlen(device):
     o, fin = w.run(algo="chunked")
     longest = int(np.argmax(lengths))
     _check(w, o, fin, BF16_TOL, seqs=[0, 7, longest, 63], heads=[0, 5, 15], tag="c4 chunked")
+
+
+@pytest.mark.parametrize("algo,dtype", [("chunked", torch.bfloat16), ("recurrent", torch.float32)])
+def test_state_in_place(device, algo, dtype):
+    """final_state may be the initial_state buffer: the result is the same as
+    with separate buffers, bit for bit, for dense and packed batches (each
+    thread reads its slice of the state before it writes the same slice)."""
+    for kw in (dict(batch=2, seq_len=150), dict(lengths=[70, 0, 130])):
+        w = Prefill(heads=3, d_k=128, d_v=128 if algo == "chunked" else 96, dtype=dtype, device=device,
+                    state_std=0.02, **kw)
+        o_sep, fin_sep = w.run(algo=algo)  # separate initial and final buffers
+        state = w.init.clone()
+        saved, w.init = w.init, state
+        try:
+            o_in, fin_in = w.run(algo=algo, final_state=state)  # initial_state is final_state
+        finally:
+            w.init = saved
+        assert fin_in.data_ptr() == state.data_ptr()
+        assert torch.equal(o_in, o_sep) and torch.equal(state, fin_sep), f"{algo} {kw}"
