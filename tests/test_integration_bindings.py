@@ -1,0 +1,144 @@
+"""The Rust bindings written out for maintainers agree with the C header.
+
+INTEGRATION.md holds the `src/sys.rs` a maintainer would add to the reference
+(crates/rhizome-gdr-hip); no Rust toolchain exists here to compile it.  This
+test parses both texts and checks, declaration by declaration, what a
+`#[repr(C)]` binding depends on: every constant's value, every struct's fields
+in order with their C types, and every function's parameters and result.
+"""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rhizome_gdr.h")
+DOC = os.path.join(ROOT, "INTEGRATION.md")
+
+# C type (const, base, pointer depth) -> Rust type in sys.rs
+SCALARS = {"int32_t": "i32", "int64_t": "i64", "uint64_t": "u64", "size_t": "usize", "float": "f32",
+           "double": "f64", "rhz_status": "i32"}
+POINTEES = {"void": "c_void", "char": "c_char", "int32_t": "i32", "float": "f32", "size_t": "usize"}
+
+
+def c_to_rust(ctype):
+    t = ctype.strip()
+    const = t.startswith("const ")
+    if const:
+        t = t[len("const "):].strip()
+    ptr = t.endswith("*")
+    base = t.rstrip("*").strip()
+    if not ptr:
+        assert not const, ctype
+        return SCALARS[base]
+    inner = POINTEES.get(base, base)  # struct pointers keep the struct's name
+    return ("*const " if const else "*mut ") + inner
+
+
+def strip_c_comments(text):
+    return re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+
+
+def parse_header():
+    text = strip_c_comments(open(HEADER).read())
+    consts = {}
+    for body in re.findall(r"typedef enum \w+ \{(.*?)\}", text, flags=re.S):
+        for name, value in re.findall(r"(RHZ_\w+)\s*=\s*(\d+)", body):
+            consts[name] = int(value)
+    for name, value in re.findall(r"#define (RHZ_\w+) (\d+)", text):
+        consts[name] = int(value)
+    structs = {}
+    for name, body in re.findall(r"typedef struct (\w+) \{(.*?)\} \1;", text, flags=re.S):
+        fields = []
+        for decl in body.split(";"):
+            decl = " ".join(decl.split())
+            if not decl:
+                continue
+            m = re.fullmatch(r"(.+?)\s*(\w+)", decl)
+            fields.append((m.group(2), c_to_rust(m.group(1))))
+        structs[name] = fields
+    funcs = {}
+    for ret, name, params in re.findall(r"(rhz_status|int32_t|const char\*)\s+(rhz_\w+)\(([^)]*)\);", text):
+        ps = []
+        for p in params.split(","):
+            p = " ".join(p.split())
+            if p in ("void", ""):
+                continue
+            m = re.fullmatch(r"(.+?)\s*(\w+)", p)
+            ps.append((m.group(2), c_to_rust(m.group(1))))
+        funcs[name] = (ps, c_to_rust(ret))
+    return consts, structs, funcs
+
+
+def sys_rs_block():
+    doc = open(DOC).read()
+    i = doc.index("### src/sys.rs")
+    start = doc.index("```rust", i) + len("```rust")
+    return doc[start:doc.index("```", start)]
+
+
+def parse_rust():
+    text = re.sub(r"//[^\n]*", "", sys_rs_block())
+    consts = {n: int(v) for n, v in re.findall(r"pub const (RHZ_\w+): i32 = (\d+);", text)}
+    structs = {}
+    for name, body in re.findall(r"#\[repr\(C\)\]\s*pub struct (\w+) \{(.*?)\}", text, flags=re.S):
+        fields = []
+        for f in body.split(","):
+            f = " ".join(f.split())
+            if f:
+                m = re.fullmatch(r"pub (\w+): (.+)", f)
+                fields.append((m.group(1), m.group(2)))
+        structs[name] = fields
+    funcs = {}
+    for name, params, ret in re.findall(r"pub fn (rhz_\w+)\(([^)]*)\)\s*->\s*([^;]+);", text, flags=re.S):
+        ps = []
+        for p in params.split(","):
+            p = " ".join(p.split())
+            if p:
+                m = re.fullmatch(r"(\w+): (.+)", p)
+                ps.append((m.group(1), m.group(2)))
+        funcs[name] = (ps, ret.strip())
+    return consts, structs, funcs
+
+
+@pytest.fixture(scope="module")
+def both():
+    return parse_header(), parse_rust()
+
+
+def test_header_parses(both):
+    (consts, structs, funcs), _ = both
+    # guards the parser itself: everything the header declares was found
+    assert len(structs) == 6 and len(funcs) == 12 and consts["RHZ_ERR_HIP"] == 4
+
+
+def test_every_constant(both):
+    (cc, _, _), (rc, _, _) = both
+    assert rc == cc
+
+
+def test_every_struct_field_in_order(both):
+    (_, cs, _), (_, rs, _) = both
+    assert sorted(rs) == sorted(cs)
+    for name in cs:
+        assert rs[name] == cs[name], name
+
+
+def test_every_function_signature(both):
+    (_, _, cf), (_, _, rf) = both
+    assert sorted(rf) == sorted(cf)
+    for name, (params, ret) in cf.items():
+        rparams, rret = rf[name]
+        assert [t for _, t in rparams] == [t for _, t in params], name
+        assert rret == ret, name
+
+
+def test_a_planted_mismatch_is_found():
+    # the comparison is not vacuous: swapping two fields of the prefill
+    # struct in the header's parse makes the struct check fail
+    (cc, cs, cf) = parse_header()
+    (rc, rs, rf) = parse_rust()
+    f = list(cs["rhz_gdr_prefill_args"])
+    f[0], f[1] = f[1], f[0]
+    assert rs["rhz_gdr_prefill_args"] != f
+    assert [n for n, _ in rs["rhz_gdr_prefill_args"]] == [n for n, _ in cs["rhz_gdr_prefill_args"]]
