@@ -46,6 +46,11 @@ def test_config0(device, algo, dtype, tol):
     dict(batch=3, heads=1, seq_len=63, d_k=32, d_v=96),
     dict(batch=1, heads=2, seq_len=200, d_k=128, d_v=256),
     dict(batch=2, heads=2, seq_len=129, d_k=16, d_v=8),
+    # key widths padded inside the chunked kernel (to 64 and 128) and value
+    # widths that end inside a 32-row tile
+    dict(batch=2, heads=1, seq_len=70, d_k=40, d_v=24),
+    dict(batch=1, heads=2, seq_len=130, d_k=96, d_v=40),
+    dict(batch=1, heads=1, seq_len=300, d_k=120, d_v=136),
 ])
 def test_shapes(device, algo, dtype, tol, shape):
     w = Prefill(**shape, dtype=dtype, device=device, state_std=0.02)
@@ -96,6 +101,20 @@ def test_value_magnitudes(device, algo, dtype, tol, scale):
     w.init64 = w.init.double().cpu().numpy()
     o, fin = w.run(algo=algo)
     _check(w, o, fin, tol, tag=f"scale {scale} {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
+@pytest.mark.parametrize("z_mean", [6.0, -6.0])
+def test_gate_extremes(device, algo, dtype, tol, z_mean):
+    """g = -softplus(z), z ~ N(z_mean, 1): z_mean 6 gives alpha ~ 0.003 (the
+    state is forgotten within a few tokens), z_mean -6 gives alpha ~ 0.998
+    (the state builds up over the whole sequence).  The chunk decays then
+    span many orders of magnitude, and the chunked path's fp16 operands are
+    rescaled as the state shrinks or grows."""
+    w = Prefill(batch=1, heads=2, seq_len=520, d_k=128, d_v=64, dtype=dtype, device=device,
+                state_std=0.02, g_mean=z_mean)
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"z_mean {z_mean} {algo} {dtype}")
 
 
 @pytest.mark.parametrize("algo,dtype", [("chunked", torch.bfloat16), ("recurrent", torch.float32)])
