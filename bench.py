@@ -50,6 +50,26 @@ DECODE = dict(batch=256, heads=16, d_k=128, d_v=128, steps=64)
 MULTISTEP = dict(batch=256, heads=16, d_k=128, d_v=128, positions=8)
 
 
+def device_info(torch) -> dict:
+    """Name, compute units and peak shader clock of GPU 0, and the dense
+    fp16/bf16 MFMA peak those give (4096 flop per CU per clock on gfx950),
+    beside the published figure the roofline uses."""
+    props = torch.cuda.get_device_properties(0)
+    info = {"name": torch.cuda.get_device_name(0), "compute_units": props.multi_processor_count}
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        khz = ctypes.c_int(0)
+        # hipDeviceGetAttribute(&v, hipDeviceAttributeClockRate (= 5), device 0): kHz
+        if hip.hipDeviceGetAttribute(ctypes.byref(khz), 5, 0) == 0 and khz.value > 0:
+            info["peak_clock_mhz"] = khz.value / 1000.0
+            info["mfma_peak_at_clock_tflops"] = props.multi_processor_count * khz.value * 1e3 * 4096 / 1e12
+    except OSError:
+        pass
+    info["mfma_peak_used_tflops"] = PEAK_MFMA_TFLOPS
+    info["hbm_peak_used_gbs"] = PEAK_HBM_GBS
+    return info
+
+
 def prefill_flops(lengths, heads, dk, dv, chunk=64) -> float:
     total = 0
     for n in lengths:
@@ -404,7 +424,7 @@ def main() -> int:
                                    "kernel": "gdr_multistep_kernel<8,2,true,float>",
                                    "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
         "prologue_epilogue": aux,
-        "device": torch.cuda.get_device_name(0),
+        "device": device_info(torch),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(pre_host, dec_host)
