@@ -61,8 +61,12 @@ typedef enum rhz_gate { RHZ_GATE_LOG_ALPHA = 0, RHZ_GATE_ALPHA = 1 } rhz_gate;
 
 /* Prefill algorithm.  AUTO picks CHUNKED for bf16 and RECURRENT for fp32.
  * RECURRENT: token-sequential fp32 recurrence (the fp32-input path).
- * CHUNKED:   64-token chunks, WY/UT transform, bf16 MFMA with fp32
- *            accumulation and fp32 state (bf16 inputs only). */
+ * CHUNKED:   64-token chunks, WY/UT transform on fp16 MFMA with fp32
+ *            accumulation and fp32 state (bf16 inputs only, converted to
+ *            fp16 on chip).  q and k are expected L2-normalised, as the
+ *            reference's op takes them (delta.rs:17), so that every element
+ *            lies within fp16's range; the state and intermediate products
+ *            are rescaled by powers of two and have no such limit. */
 typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUNKED = 2 } rhz_algo;
 
 /* Op identities for rhz_gdr_query_support, named after the plan-level ops
