@@ -104,6 +104,18 @@ def test_value_magnitudes(device, algo, dtype, tol, scale):
 
 
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)
+def test_query_scaled_by_sqrt_dk(device, algo, dtype, tol):
+    """q as the prologue hands it over, l2norm(q) * sqrt(d_k) (rhz_gdr_prepare,
+    SPEC.md:53): rows of norm 11.3 at d_k = 128."""
+    w = Prefill(batch=2, heads=2, seq_len=200, d_k=128, d_v=64, dtype=dtype, device=device,
+                state_std=0.02)
+    w.q = (w.q.double() * np.sqrt(128.0)).to(dtype)
+    w.q64 = w.q.double().cpu().numpy()
+    o, fin = w.run(algo=algo)
+    _check(w, o, fin, tol, tag=f"q * sqrt(d_k) {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
 @pytest.mark.parametrize("z_mean", [6.0, -6.0])
 def test_gate_extremes(device, algo, dtype, tol, z_mean):
     """g = -softplus(z), z ~ N(z_mean, 1): z_mean 6 gives alpha ~ 0.003 (the
