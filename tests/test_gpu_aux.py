@@ -106,3 +106,50 @@ def test_rmsnorm_in_place_and_heads_independent(device):
     y = rhizome_amd.rmsnorm_heads(x, torch.ones(2, device=device), 1e-12, out=x)
     torch.cuda.synchronize()
     assert abs(float(y[0, 0]) - float(y[1, 0])) < 1e-6 and y.data_ptr() == x.data_ptr()
+
+
+@pytest.mark.parametrize("dtype,algo,tol", [(torch.bfloat16, "chunked", BF16_TOL),
+                                            (torch.float32, "recurrent", F32_TOL)])
+def test_local_block_chain(device, dtype, algo, tol):
+    """conv1d over each of the q, k, v projections -> prepare -> prefill ->
+    per-head RMSNorm, each stage reading the previous stage's device output
+    as it lies (views only, no copies between the library calls), packed
+    sequences throughout.  Every stage is checked against the oracle applied
+    to the device's own input of that stage, so each stage's tolerance is its
+    own."""
+    rng = _rng(21)
+    H, dk, dv = 4, 64, 64
+    lengths = [70, 0, 130, 5]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    n_tok = int(cu[-1])
+    cu_dev = torch.from_numpy(cu.astype(np.int32)).to(device)
+    conv = {}
+    for name, d in (("q", dk), ("k", dk), ("v", dv)):
+        x, x64 = to_device(rng.normal(size=(n_tok, H * d)), dtype, device)
+        w, w64 = to_device(rng.normal(scale=0.5, size=(H * d, 4)), torch.float32, device)
+        y, _ = rhizome_amd.causal_conv1d(x, w, cu_seqlens=cu_dev)
+        ry, _ = O.conv1d_batched(cu, x64, w64, None, None)
+        y64 = y.double().cpu().numpy()
+        check_close(y64, ry, tol, f"chain conv1d {name}")
+        conv[name] = (y.view(n_tok, H, d), y64.reshape(n_tok, H, d))
+    bl, bl64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    al, al64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    a, a64 = to_device(rng.normal(size=H), torch.float32, device)
+    q, k, beta, g = rhizome_amd.prepare(conv["q"][0], conv["k"][0], bl, al, a)
+    rq, rk, rb, rg = O.prepare(conv["q"][1], conv["k"][1], bl64, al64, a64, float(dk) ** 0.5)
+    q64, k64 = q.double().cpu().numpy(), k.double().cpu().numpy()
+    b64, g64 = beta.double().cpu().numpy(), g.double().cpu().numpy()
+    check_close(q64, rq, tol, "chain prepare q")
+    check_close(k64, rk, tol, "chain prepare k")
+    check_close(b64, rb, F32_TOL, "chain prepare beta")
+    check_close(g64, rg, F32_TOL, "chain prepare g")
+    o, fin = rhizome_amd.prefill(q, k, conv["v"][0], g, beta, cu_seqlens=cu_dev, algo=algo)
+    ro, rf = O.prefill_batched(cu, q64, k64, conv["v"][1], np.exp(g64), b64, None)
+    check_close(o.double().cpu().numpy(), ro, tol, "chain prefill o")
+    check_close(fin.cpu().numpy(), rf, tol, "chain prefill final state")
+    s, s64 = to_device(rng.normal(size=dv), torch.float32, device)
+    out = rhizome_amd.rmsnorm_heads(o.view(n_tok * H, dv), s, 1e-6)
+    torch.cuda.synchronize()
+    rr = O.rmsnorm_rows(o.double().cpu().numpy().reshape(n_tok * H, dv), s64, 1e-6)
+    m = check_close(out.double().cpu().numpy(), rr, tol, "chain rmsnorm")
+    print(f"local block chain {dtype} {algo}: rmsnorm {m}", flush=True)
