@@ -187,8 +187,11 @@ __global__ __launch_bounds__(256) void gdr_decode_kernel(StepParams p) {
 
 // ------------------------------------------------------------- multistep
 // Grid: x = b*H + h, y = block of P*RPP rows, as the decode kernel; the rows
-// stay in registers across the n positions, and each position's k, q, v and
-// gates are loaded while the previous one is applied.
+// stay in registers across the n positions.  Each position's k, q, v and
+// gates are loaded when it starts: without a second register set for the
+// next position the kernel needs 92 VGPRs instead of 125, and the fifth wave
+// per SIMD this allows hides the load latency better than prefetching did
+// (473.7 vs 480.1 us at B = 256, H = 16, d = 128, 8 positions).
 template <int LPR, int P, bool VEC, typename T>
 __global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
     constexpr int RPP = 256 / LPR;
@@ -230,8 +233,8 @@ __global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
         gn = p.gate[th];
         bn = p.beta[th];
     };
-    fetch(0);
     for (int t = 0; t < n; ++t) {
+        fetch(t);
         float kr[16], qr[16], vr[P];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -241,7 +244,6 @@ __global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) vr[pp] = vn[pp];
         const float ga = gn, be = bn;
-        if (t + 1 < n) fetch(t + 1);
         const float alpha = decay_factor(ga, p.gate_is_alpha);
         const float kq = group_sum<LPR>(dot16(kr, qr));
         const long th = ((long)b * n + t) * H + h;
