@@ -51,6 +51,9 @@ def test_config0(device, algo, dtype, tol):
     dict(batch=2, heads=1, seq_len=70, d_k=40, d_v=24),
     dict(batch=1, heads=2, seq_len=130, d_k=96, d_v=40),
     dict(batch=1, heads=1, seq_len=300, d_k=120, d_v=136),
+    # the widest value rows the ABI takes, and many heads
+    dict(batch=1, heads=1, seq_len=100, d_k=128, d_v=1024),
+    dict(batch=1, heads=64, seq_len=66, d_k=32, d_v=32),
 ])
 def test_shapes(device, algo, dtype, tol, shape):
     w = Prefill(**shape, dtype=dtype, device=device, state_std=0.02)
