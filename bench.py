@@ -93,6 +93,9 @@ PROFILES = {
     "prefill": "gdr_chunk_kernel_128_prefill_b4_h16_t4096_d128.md",
     "decode": "gdr_decode_kernel_decode_b256_h16_d128.md",
     "multistep": "gdr_multistep_kernel_b256_h16_d128_n8.md",
+    "conv1d": "conv1d_kernel_bf16_t16384_c6144.md",
+    "prepare": "prepare_kernel_bf16_t16384_h16_d128.md",
+    "rmsnorm": "rmsnorm_kernel_bf16_rows262144_d128.md",
 }
 
 
@@ -266,8 +269,9 @@ def bench_aux(torch, steps, warmup):
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"value": gbs, "unit": "GB/s", "ms_per_step": ms, "workload": shape,
                      "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                                  "frac": gbs / PEAK_HBM_GBS, "kernel": kernel,
-                                  "bytes_per_launch": float(nbytes), "launch_us": ms * 1e3}}
+                                  "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles(name),
+                                  "kernel": kernel, "bytes_per_launch": float(nbytes),
+                                  "launch_us": ms * 1e3}}
     return out
 
 
