@@ -474,12 +474,25 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, 
             *reinterpret_cast<uint4*>(&sm.k[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8(r.k[u]);
             *reinterpret_cast<uint4*>(&sm.q[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8(r.q[u]);
         }
+        // beta V^T in 8-byte writes of two tokens: lane l (token 2m + odd)
+        // and lane l ^ 4 (the other token of the pair, same 8 state rows)
+        // swap four values, then the even lane writes rows c8 + 0..3 and
+        // the odd lane rows c8 + 4..7, both at tokens 2m, 2m + 1.
         const int row = lt >> 2, c8 = (lt & 3) * 8;
+        const bool odd = row & 1;
         const uint32_t wv[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+        float val[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            sm.vb[NB][(c8 + 2 * e) * kLDV + row] = r.bv * __uint_as_float(wv[e] << 16);
-            sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = r.bv * __uint_as_float(wv[e] & 0xffff0000u);
+            val[2 * e] = r.bv * __uint_as_float(wv[e] << 16);
+            val[2 * e + 1] = r.bv * __uint_as_float(wv[e] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // lane ^ 4: row_half_mirror, then quad_perm [3, 2, 1, 0]
+            const float recv = dpp_mov<0x1B>(dpp_mov<0x141>(odd ? val[k] : val[4 + k]));
+            const float2 pair = odd ? make_float2(recv, val[4 + k]) : make_float2(val[k], recv);
+            *reinterpret_cast<float2*>(&sm.vb[NB][(c8 + k + (odd ? 4 : 0)) * kLDV + row - (odd ? 1 : 0)]) = pair;
         }
     } else {
         const uint4 z = make_uint4(0, 0, 0, 0);
@@ -615,8 +628,16 @@ __device__ __forceinline__ void t_diag(Smem<DK>& sm, int l) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) t[r] = r == col ? 1.f : 0.f;
     t_diag_solve(t, a, col, std::make_integer_sequence<int, 15>{});
+    // 4-byte writes of two columns: lane col and lane col ^ 1 swap eight
+    // values, then the even lane writes rows 0..7 and the odd lane rows
+    // 8..15, both at columns col & ~1, (col & ~1) + 1.
+    const bool odd = col & 1;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sm.t[NB][toff(16 * blk + r, 16 * blk + col)] = f32_to_f16(t[r]);
+    for (int k = 0; k < 8; ++k) {
+        const float recv = dpp_mov<0xB1>(odd ? t[k] : t[8 + k]);  // quad_perm [1, 0, 3, 2]
+        *reinterpret_cast<uint32_t*>(&sm.t[NB][toff(16 * blk + k + (odd ? 8 : 0), 16 * blk + (col & ~1))]) =
+            pack_f16x2(odd ? recv : t[k], odd ? t[8 + k] : recv);
+    }
 }
 
 // T_ij = -T_ii (sum_{m=j}^{i-1} A_im T_mj) for one 16x16 block of T (buffer
