@@ -955,7 +955,9 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
             Bu[kk] = pack8(U[2 * kk], U[2 * kk + 1]);
             Bh[kk] = pack8(U[2 * kk] * gd[2 * kk], U[2 * kk + 1] * gd[2 * kk + 1]);
         }
-        // S update: K^T through transposed reads, 2 column blocks ahead.
+        // S update: K^T through transposed reads, 4 column blocks ahead (the
+        // earlier the last read of buffer B, the sooner it is refilled:
+        // measured 1.8 % faster than 2 ahead, and faster than 3, 5 or 6).
         s16x4 kt[NJ][4];
         auto kt_load = [&](int jb) {
             const int col = 32 * (jb >> 1) + 8 * (n & 3) + 4 * (jb & 1);
@@ -966,7 +968,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
                 kt[jb][2 * kk + 1] = ld_tr(&sm.k[B][KQ<DK>::off(row + 4, col)]);
             }
         };
-        constexpr int kAhead = NJ < 2 ? NJ : 2;
+        constexpr int kAhead = NJ < 4 ? NJ : 4;
         // The last read of buffer B is issued in S-update step kLastRead
         // (before the loop when negative); once it has returned the buffer is
         // free, so the chunk is counted there, ahead of the remaining MFMAs,
