@@ -46,7 +46,15 @@ PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 PREFILL = dict(batch=4, heads=16, seq_len=4096, d_k=128, d_v=128, chunk=64)
+# long context, slow decay: g = -softplus(N(-2, 1))
+PREFILL_LONG = dict(batch=1, heads=32, seq_len=32768, d_k=128, d_v=256, chunk=64, g_mean=-2.0)
+# 64 packed sequences, lengths 128 + floor(u * 8065) from Philox stream 7,
+# initial states N(0, 0.02)
+PREFILL_VARLEN = dict(n_seqs=64, heads=16, d_k=128, d_v=128, chunk=64, len_lo=128, len_hi=8192,
+                      state_std=0.02)
 DECODE = dict(batch=256, heads=16, d_k=128, d_v=128, steps=64)
+# the same step with a 1.07 GB state, over 4x the 256 MB last-level cache
+DECODE_LARGE = dict(batch=1024, heads=16, d_k=128, d_v=128, steps=16)
 MULTISTEP = dict(batch=256, heads=16, d_k=128, d_v=128, positions=8)
 
 
@@ -91,7 +99,10 @@ def decode_bytes(batch, heads, dk, dv) -> float:
 
 PROFILES = {
     "prefill": "gdr_chunk_kernel_128_prefill_b4_h16_t4096_d128.md",
+    "prefill_long": "gdr_chunk_kernel_128_prefill_b1_h32_t32768_dk128_dv256.md",
+    "prefill_varlen": "gdr_chunk_kernel_128_prefill_varlen64_h16_d128.md",
     "decode": "gdr_decode_kernel_decode_b256_h16_d128.md",
+    "decode_large": "gdr_decode_kernel_decode_b1024_h16_d128.md",
     "multistep": "gdr_multistep_kernel_b256_h16_d128_n8.md",
     "conv1d": "conv1d_kernel_bf16_t16384_c6144.md",
     "prepare": "prepare_kernel_bf16_t16384_h16_d128.md",
@@ -118,6 +129,25 @@ def multistep_bytes(batch, heads, dk, dv, n) -> float:
     return float(batch * heads * (4 * dk * dv * (1 + n) + n * (4 * (2 * dk + 2 * dv) + 8)))
 
 
+SETTLE_MS = 150.0  # wall time of untimed launches before each leg's counted warmup
+
+
+def settle(torch, fn, ms: float = SETTLE_MS) -> dict:
+    """Runs fn back to back for at least `ms` of wall time before anything is
+    counted.  The GPU's clocks ramp up over the first tens of milliseconds of
+    sustained work; without this, a short counted warmup leaves the timed
+    launches on a rising clock.  Nothing here is timed or reported as a
+    result: the JSON line only records how long the settle phase ran."""
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        n += 10
+        torch.cuda.synchronize()
+    return {"settle_ms": (time.perf_counter() - t0) * 1e3, "settle_launches": n}
+
+
 def time_region(torch, stream, fn, reps: int) -> float:
     """Milliseconds per call of fn over reps calls, HIP events on `stream`."""
     start = torch.cuda.Event(enable_timing=True)
@@ -131,23 +161,45 @@ def time_region(torch, stream, fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def bench_prefill(torch, steps, warmup):
+def varlen_lengths_dev(torch, n, lo, hi, seed=0):
+    """Seeded lengths lo + floor(u (hi - lo + 1)), u = next_f64 #i of Philox
+    stream 7 (rng.rs:78-82), drawn on the device."""
+    u = __import__("rhizome_amd").philox_fill("uniform", seed, 7, (n,), torch.float64)
+    return [int(x) for x in (lo + torch.floor(u * (hi - lo + 1))).cpu().tolist()]
+
+
+def bench_prefill(torch, steps, warmup, c=None):
+    """One prefill leg: a dense batch (batch, seq_len) or a packed one
+    (lengths, with per-sequence initial states).  Returns the timing, the
+    algorithmic work and the device inputs."""
     import rhizome_amd
     from rhizome_amd import _abi, gdr
 
-    c = PREFILL
-    B, T, H, dk, dv = c["batch"], c["seq_len"], c["heads"], c["d_k"], c["d_v"]
+    c = c or PREFILL
+    H, dk, dv = c["heads"], c["d_k"], c["d_v"]
     dev = torch.device("cuda:0")
     bf16, f32 = torch.bfloat16, torch.float32
-    q = rhizome_amd.philox_fill("unit_rows", 0, 1, (B, T, H, dk), bf16)
-    k = rhizome_amd.philox_fill("unit_rows", 0, 2, (B, T, H, dk), bf16)
-    v = rhizome_amd.philox_fill("normal", 0, 3, (B, T, H, dv), bf16)
-    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, (B, T, H), f32)
-    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, (B, T, H), f32)
-    o = torch.empty((B, T, H, dv), dtype=bf16, device=dev)
-    fin = torch.empty((B, H, dv, dk), dtype=f32, device=dev)
-    args = gdr.prefill_args(q, k, v, g, beta, _abi.GATE_LOG_ALPHA, None, None, fin, o, "chunked")
-    ws = torch.empty(gdr.workspace_bytes(args), dtype=torch.uint8, device=dev)
+    if "lengths" in c:
+        lengths = c["lengths"]
+        n_tok, lead = sum(lengths), (sum(lengths),)
+        cu = torch.tensor([0] + list(__import__("itertools").accumulate(lengths)), dtype=torch.int32,
+                          device=dev)
+        n_seq = len(lengths)
+    else:
+        B, T = c["batch"], c["seq_len"]
+        lengths, n_tok, lead, cu, n_seq = [T] * B, B * T, (B, T), None, B
+    q = rhizome_amd.philox_fill("unit_rows", 0, 1, lead + (H, dk), bf16)
+    k = rhizome_amd.philox_fill("unit_rows", 0, 2, lead + (H, dk), bf16)
+    v = rhizome_amd.philox_fill("normal", 0, 3, lead + (H, dv), bf16)
+    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, lead + (H,), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, lead + (H,), f32, mean=c.get("g_mean", 0.0))
+    init = None
+    if c.get("state_std"):
+        init = rhizome_amd.philox_fill("normal", 0, 6, (n_seq, H, dv, dk), f32, std=c["state_std"])
+    o = torch.empty(lead + (H, dv), dtype=bf16, device=dev)
+    fin = torch.empty((n_seq, H, dv, dk), dtype=f32, device=dev)
+    args = gdr.prefill_args(q, k, v, g, beta, _abi.GATE_LOG_ALPHA, cu, init, fin, o, "chunked")
+    ws = torch.empty(max(gdr.workspace_bytes(args), 256), dtype=torch.uint8, device=dev)
     args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     stream = torch.cuda.current_stream()
     lib, argp, sp = _abi.lib(), ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream or None)
@@ -157,20 +209,43 @@ def bench_prefill(torch, steps, warmup):
         if st:
             _abi.check(st)
 
+    info = settle(torch, step)
     for _ in range(warmup):
         step()
     ms = time_region(torch, stream, step, steps)
-    flops = prefill_flops([T] * B, H, dk, dv)
-    algo_bytes = prefill_bytes(B * T, H, dk, dv, B)
-    host = {"q": q, "k": k, "v": v, "g": g, "beta": beta}
+    if rhizome_amd.sync_timeouts() != 0:
+        raise RuntimeError("a chunked-kernel LDS wait gave up during the benchmark")
+    flops = prefill_flops(lengths, H, dk, dv)
+    algo_bytes = prefill_bytes(n_tok, H, dk, dv, n_seq, init_state=init is not None)
+    host = {"q": q, "k": k, "v": v, "g": g, "beta": beta, "tokens": n_tok, **info}
     return ms, flops, algo_bytes, host
 
 
-def bench_decode(torch, warmup):
+def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
+    """A secondary prefill workload as its own JSON object."""
+    ms, flops, nbytes, host = bench_prefill(torch, steps, warmup, c)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    cfg = {k: v for k, v in c.items() if k != "lengths"}
+    if "lengths" in c:
+        cfg.update(n_seqs=len(c["lengths"]), tokens=host["tokens"], min_len=min(c["lengths"]),
+                   max_len=max(c["lengths"]))
+    return {"metric": "GDR prefill tokens/s", "value": host["tokens"] / (ms * 1e-3), "unit": "tokens/s",
+            "ms_per_step": ms, "steps": steps, "settle_ms": host["settle_ms"],
+            "config": {"workload": workload, **cfg},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles(profile_key),
+                         "kernel": "gdr_chunk_kernel<128>", "algorithmic_bytes": nbytes,
+                         "launch_us": ms * 1e3,
+                         "mfma": {"achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": tflops / PEAK_MFMA_TFLOPS, "flops_per_launch": flops}}}
+
+
+def bench_decode(torch, warmup, c=None):
     import rhizome_amd
     from rhizome_amd import _abi, gdr
 
-    c = DECODE
+    c = c or DECODE
     B, H, dk, dv, n = c["batch"], c["heads"], c["d_k"], c["d_v"], c["steps"]
     f32 = torch.float32
     q = rhizome_amd.philox_fill("unit_rows", 0, 1, (n, B, H, dk), f32)
@@ -194,10 +269,11 @@ def bench_decode(torch, warmup):
         if st:
             _abi.check(st)
 
+    info = settle(torch, step)
     for _ in range(warmup):
         step()
     ms = time_region(torch, stream, step, n)
-    return ms, decode_bytes(B, H, dk, dv), {"q": q, "k": k, "v": v, "g": g, "beta": beta}
+    return ms, decode_bytes(B, H, dk, dv), {"q": q, "k": k, "v": v, "g": g, "beta": beta, **info}
 
 
 def bench_multistep(torch, steps, warmup):
@@ -224,6 +300,7 @@ def bench_multistep(torch, steps, warmup):
         if st:
             _abi.check(st)
 
+    settle(torch, step, SETTLE_MS / 3)
     for _ in range(warmup):
         step()
     ms = time_region(torch, stream, step, steps)
@@ -263,6 +340,7 @@ def bench_aux(torch, steps, warmup):
     }
     out = {}
     for name, (fn, nbytes, kernel, shape) in jobs.items():
+        settle(torch, fn, SETTLE_MS / 3)
         for _ in range(warmup):
             fn()
         ms = time_region(torch, stream, fn, steps)
@@ -314,6 +392,10 @@ def cpu_baseline(pre_host, dec_host):
         "value": B * T / t_all,
         "unit": "tokens/s",
         "cores": cores,
+        # the thread count is capped at 16, the host CPU share that one GPU
+        # of the box is given, whatever the affinity mask shows
+        "cores_available": len(os.sched_getaffinity(0)),
+        "cores_cap": O.MAX_THREADS,
         "kind": "port",
         "sample": (f"full prefill workload (B={B} H={H} T={T} d={dk}, {B * H} heads) through "
                    "the f64 oracle's gated_delta_sequential, heads spread over all cores"),
@@ -351,8 +433,9 @@ def _cpu_model() -> str:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU clock ramps up over the first ~20 ms of back-to-back launches:
-    # the warmup covers that, so the timed steps run at steady clocks
+    # each leg first runs SETTLE_MS of untimed launches (the GPU clock ramps
+    # up over the first tens of ms of back-to-back launches), then the
+    # counted warmup, then the timed steps
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -371,8 +454,16 @@ def main() -> int:
         return 1
     ms, flops, algo_bytes, pre_host = bench_prefill(torch, args.steps, args.warmup)
     dms, dbytes, dec_host = bench_decode(torch, args.warmup)
+    dlms, dlbytes, _ = bench_decode(torch, min(args.warmup, 16), DECODE_LARGE)
     mms, mbytes = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
     aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
+    long_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), PREFILL_LONG,
+                           "chunked GDR prefill, long context, slow decay", "prefill_long")
+    vc = dict(PREFILL_VARLEN)
+    vc["lengths"] = varlen_lengths_dev(torch, vc["n_seqs"], vc["len_lo"], vc["len_hi"])
+    varlen_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), vc,
+                             "chunked GDR prefill, packed variable-length batch with initial states",
+                             "prefill_varlen")
     if args.calibration_copy:
         calibration_copy(torch)
     c = PREFILL
@@ -388,6 +479,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": pre_host["settle_ms"],
+        "settle_launches": pre_host["settle_launches"],
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
@@ -416,7 +509,22 @@ def main() -> int:
                                 "unit": "GB/s", "frac": dgbs / PEAK_HBM_GBS,
                                 "traffic": traffic_from_profiles("decode"),
                                 "kernel": "gdr_decode_kernel<8,4,true,float>",
-                                "bytes_per_launch": dbytes, "launch_us": dms * 1e3}},
+                                "bytes_per_launch": dbytes, "launch_us": dms * 1e3},
+                   "settle_ms": dec_host["settle_ms"]},
+        # control: the same step with the state 4x the 256 MB last-level
+        # cache, so that the decode rate above is not a cache effect
+        "decode_large_state": {
+            "metric": "decode state-update HBM GB/s", "value": dlbytes / (dlms * 1e-3) / 1e9,
+            "unit": "GB/s", "ms_per_step": dlms, "steps": DECODE_LARGE["steps"],
+            "config": {"workload": "GDR decode step, state in place, 1.07 GB state", **DECODE_LARGE,
+                       "dtype": "fp32"},
+            "roofline": {"bound": "hbm", "achieved": dlbytes / (dlms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": dlbytes / (dlms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                         "traffic": traffic_from_profiles("decode_large"),
+                         "kernel": "gdr_decode_kernel<8,4,true,float>", "bytes_per_launch": dlbytes,
+                         "launch_us": dlms * 1e3}},
+        "prefill_long_context": long_leg,
+        "prefill_varlen": varlen_leg,
         "multistep": {"metric": "multistep HBM GB/s (state read, per-position snapshots written)",
                       "value": mbytes / (mms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": mms,
                       "config": {"workload": "GDR multistep, 8 positions from a given state",

@@ -179,6 +179,24 @@ rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size
 /* Gated delta-rule prefill (see rhz_gdr_prefill_args). */
 rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream);
 
+/* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
+ * reference, whose op is a CPU loop).  The kernel's waves synchronise through
+ * LDS counters with bounded waits; a wait that gives up lets the kernel end
+ * and is counted on the device.  Writes the current device's count to *count
+ * and, when reset is nonzero, sets it to zero.  Blocking: it waits for the
+ * device's outstanding work.  A nonzero count means that some chunked launch
+ * since the last reset may have produced wrong results. */
+rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset);
+
+/* Test hook (no counterpart in the reference): rhz_gdr_prefill with the
+ * CHUNKED kernel's waits bounded at spin_limit polls (>= 1) instead of the
+ * built-in 2^20, so that a test can force give-ups and see them counted by
+ * rhz_gdr_sync_timeouts.  Same arguments and validation as rhz_gdr_prefill;
+ * the results of a call whose waits gave up are unspecified but every access
+ * stays inside the caller's buffers. */
+rhz_status rhz_gdr_prefill_spin_limit(const rhz_gdr_prefill_args* args, int32_t spin_limit,
+                                      void* stream);
+
 /* Gated delta-rule decode step (see rhz_gdr_decode_args). */
 rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* args, void* stream);
 
@@ -261,13 +279,17 @@ rhz_status rhz_rmsnorm_heads(const rhz_rmsnorm_args* args, void* stream);
  *                              (mean and std_dev unused; count % row_len == 0)
  *   RHZ_FILL_SIGMOID           sigmoid(mean + std * z)
  *   RHZ_FILL_NEG_SOFTPLUS      -softplus(mean + std * z)
+ *   RHZ_FILL_UNIFORM           u = next_f64 #e of the stream (rng.rs:78-82:
+ *                              words 2e and 2e + 1), in [0, 1); mean and
+ *                              std_dev unused
  * then rounded (f64 -> f32 -> bf16, round to nearest even) to out_dtype
  * (RHZ_F64, RHZ_F32 or RHZ_BF16). */
 typedef enum rhz_fill_kind {
     RHZ_FILL_NORMAL = 0,
     RHZ_FILL_UNIT_ROWS = 1,
     RHZ_FILL_SIGMOID = 2,
-    RHZ_FILL_NEG_SOFTPLUS = 3
+    RHZ_FILL_NEG_SOFTPLUS = 3,
+    RHZ_FILL_UNIFORM = 4
 } rhz_fill_kind;
 
 rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count,

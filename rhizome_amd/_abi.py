@@ -10,7 +10,7 @@ import ctypes
 import os
 import re
 from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int32, c_int64, c_size_t,
-                    c_uint64, c_void_p)
+                    c_uint32, c_uint64, c_void_p)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -29,7 +29,7 @@ ALGO_AUTO, ALGO_RECURRENT, ALGO_CHUNKED = 0, 1, 2
 OP_DELTA_SCAN, OP_DELTA_STEP, OP_DELTA_MULTISTEP = 0, 1, 2
 MULTISTEP_MAX = 64
 # rhz_fill_kind
-FILL_NORMAL, FILL_UNIT_ROWS, FILL_SIGMOID, FILL_NEG_SOFTPLUS = 0, 1, 2, 3
+FILL_NORMAL, FILL_UNIT_ROWS, FILL_SIGMOID, FILL_NEG_SOFTPLUS, FILL_UNIFORM = 0, 1, 2, 3, 4
 
 
 class PrefillArgs(Structure):
@@ -122,6 +122,10 @@ def lib():
         L.rhz_gdr_prefill_workspace_size.restype = c_int32
         L.rhz_gdr_prefill.argtypes = [POINTER(PrefillArgs), c_void_p]
         L.rhz_gdr_prefill.restype = c_int32
+        L.rhz_gdr_sync_timeouts.argtypes = [POINTER(c_uint32), c_int32]
+        L.rhz_gdr_sync_timeouts.restype = c_int32
+        L.rhz_gdr_prefill_spin_limit.argtypes = [POINTER(PrefillArgs), c_int32, c_void_p]
+        L.rhz_gdr_prefill_spin_limit.restype = c_int32
         L.rhz_gdr_decode_step.argtypes = [POINTER(DecodeArgs), c_void_p]
         L.rhz_gdr_decode_step.restype = c_int32
         L.rhz_gdr_multistep.argtypes = [POINTER(MultistepArgs), c_void_p]

@@ -163,10 +163,35 @@ rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size
     return ok();
 }
 
-rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) {
+namespace {
+rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit);
+}  // namespace
+
+rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) { return prefill_impl(args, stream, 0); }
+
+rhz_status rhz_gdr_prefill_spin_limit(const rhz_gdr_prefill_args* args, int32_t spin_limit, void* stream) {
+    if (spin_limit < 1) return fail(RHZ_ERR_INVALID_ARG, "spin_limit must be >= 1 (got %d)", spin_limit);
+    return prefill_impl(args, stream, spin_limit);
+}
+
+rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset) {
+    if (!count) return fail(RHZ_ERR_INVALID_ARG, "count is NULL");
+    unsigned int n = 0;
+    const hipError_t e = rhz::chunked_sync_timeouts(&n, reset != 0);
+    if (e != hipSuccess) return hip_status(e, "reading the sync timeout count");
+    *count = n;
+    return ok();
+}
+
+}  // extern "C"
+
+namespace {
+rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit) {
     int algo = 0;
     const rhz_status s = check_prefill(args, true, &algo);
     if (s != RHZ_OK) return s;
+    // No tokens and no final state: nothing to compute or write.
+    if (args->seq_len == 0 && !args->final_state) return ok();
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (algo == RHZ_ALGO_CHUNKED) {
         const size_t need = rhz::chunked_workspace_bytes(*args);
@@ -177,10 +202,13 @@ rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) {
             if (reinterpret_cast<uintptr_t>(args->workspace) & 255u)
                 return fail(RHZ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
         }
-        return hip_status(rhz::launch_chunked(*args, st), "chunked prefill launch");
+        return hip_status(rhz::launch_chunked(*args, st, spin_limit), "chunked prefill launch");
     }
     return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");
 }
+}  // namespace
+
+extern "C" {
 
 rhz_status rhz_gdr_decode_step(const rhz_gdr_decode_args* a, void* stream) {
     if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
@@ -319,7 +347,7 @@ rhz_status rhz_rmsnorm_heads(const rhz_rmsnorm_args* a, void* stream) {
 
 rhz_status rhz_philox_fill(int32_t kind, uint64_t seed, uint64_t stream_id, int64_t count, int32_t row_len,
                            double mean, double std_dev, int32_t out_dtype, void* out, void* stream) {
-    if (kind < RHZ_FILL_NORMAL || kind > RHZ_FILL_NEG_SOFTPLUS) return fail(RHZ_ERR_INVALID_ARG, "unknown kind %d", kind);
+    if (kind < RHZ_FILL_NORMAL || kind > RHZ_FILL_UNIFORM) return fail(RHZ_ERR_INVALID_ARG, "unknown kind %d", kind);
     if (count < 0) return fail(RHZ_ERR_INVALID_ARG, "count must be >= 0");
     if (out_dtype != RHZ_F32 && out_dtype != RHZ_BF16 && out_dtype != RHZ_F64)
         return fail(RHZ_ERR_INVALID_ARG, "out_dtype must be RHZ_F64, RHZ_F32 or RHZ_BF16");

@@ -448,7 +448,9 @@ hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t st) {
         if (e != hipSuccess) return e;
     }
     if (a.final_state) {
-        hipLaunchKernelGGL(conv1d_empty_kernel, dim3(ncb, min(a.batch, 65535)), dim3(256), 0, st, p);
+        // one channel per thread, whatever the main kernel's vector width
+        const int ecb = (a.channels + 255) / 256;
+        hipLaunchKernelGGL(conv1d_empty_kernel, dim3(ecb, min(a.batch, 65535)), dim3(256), 0, st, p);
         return hipGetLastError();
     }
     return hipSuccess;

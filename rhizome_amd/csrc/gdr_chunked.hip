@@ -65,6 +65,9 @@
 namespace rhz {
 namespace {
 
+// Number of LDS waits that gave up since the last reset (per device).
+__device__ unsigned int g_sync_timeouts;
+
 constexpr int kTV = 32;           // rows of S per workgroup (two scan waves of 16)
 constexpr int kMaxSortSeqs = 4096;
 constexpr int kMaxScaleExp = 60;  // bound on one rescaling step
@@ -92,7 +95,8 @@ struct ChunkParams {
     uint16_t* o;
     const int* order;  // [N] longest-first (packed batches), nullptr for dense
     int batch, seq_len, heads, d_k, d_v, gate_is_alpha;
-    int n_tiles;  // ceil(d_v / 32)
+    int n_tiles;     // ceil(d_v / 32)
+    int spin_limit;  // polls after which an LDS wait gives up (and is counted)
 };
 
 // LDS tile addressing.  Rows are unpadded and the 16-byte chunks of a row
@@ -295,8 +299,11 @@ __device__ __forceinline__ void map_block(int bid, int units, int nt, int& unit,
 // needs all of them); the two scan waves can, so each has its own counter.
 // Every wait is for a step of an earlier or the same chunk of another role,
 // and each role processes its chunks in order, so the waits form an acyclic
-// graph; a wait also gives up after kSpinLimit polls, so the kernel ends even
-// if that property were ever broken.
+// graph; a wait also gives up after spin_limit polls, so the kernel ends even
+// if that property were ever broken.  A wait that gives up adds 1 to
+// g_sync_timeouts (one lane, a vector atomic), which the host reads through
+// rhz_gdr_sync_timeouts: a nonzero count means the results of that launch
+// may be wrong.
 struct Sync {
     int staged;  // loader waves (4 per chunk): K, Q, beta V, gates in LDS
     int tdiag;   // wave 2 (1 per chunk): K K^T diagonal blocks and T's diagonal blocks
@@ -320,7 +327,7 @@ __device__ __forceinline__ void signal(int* cnt) {
 // s_sleep between polls).
 typedef __attribute__((address_space(3))) int lds_int;
 template <int N>
-__device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) {
+__device__ __forceinline__ void wait_all(int lim, int* const (&c)[N], const int (&t)[N]) {
     const int lane = __lane_id();
     const lds_int* addr = (const lds_int*)c[0];
     int tgt = -0x7fffffff;
@@ -330,13 +337,18 @@ __device__ __forceinline__ void wait_all(int* const (&c)[N], const int (&t)[N]) 
             addr = (const lds_int*)c[i];
             tgt = t[i];
         }
-    for (int spin = 0; spin < kSpinLimit; ++spin) {
+    bool met = false;
+    for (int spin = 0; spin < lim; ++spin) {
         const int v = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (__builtin_amdgcn_ballot_w64(v < tgt) == 0) break;
+        if (__builtin_amdgcn_ballot_w64(v < tgt) == 0) {
+            met = true;
+            break;
+        }
     }
+    if (!met && lane == 0) atomicAdd(&g_sync_timeouts, 1u);
     asm volatile("" ::: "memory");
 }
-__device__ __forceinline__ void wait_ge(int* cnt, int target) { wait_all<1>({cnt}, {target}); }
+__device__ __forceinline__ void wait_ge(int lim, int* cnt, int target) { wait_all<1>(lim, {cnt}, {target}); }
 
 // Shared memory of one workgroup.  Buffers indexed [2] are double-buffered
 // by chunk parity.  T and P hold zeros above the diagonal blocks for the
@@ -673,12 +685,12 @@ __device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
 // Wave 2, chunk x (buffer B = x & 1): K K^T's diagonal blocks and T's
 // diagonal blocks, then T_10, T_20, T_30.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l) {
+__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     // K[B] staged; T[B] was read by the scan and written by both waves for chunk x - 2
     Sync& sy = sm.sync;
-    wait_all<4>({&sy.staged, &sy.scanned[0], &sy.scanned[1], &sy.tfull}, {4 * (x + 1), x - 1, x - 1, 2 * (x - 1)});
+    wait_all<4>(lim, {&sy.staged, &sy.scanned[0], &sy.scanned[1], &sy.tfull}, {4 * (x + 1), x - 1, x - 1, 2 * (x - 1)});
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
@@ -689,7 +701,7 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l) {
     lds_fence();
     t_diag<DK, B>(sm, l);
     signal(&sm.sync.tdiag);
-    wait_ge(&sm.sync.aoff, x + 1);
+    wait_ge(lim, &sm.sync.aoff, x + 1);
     t_block<DK, B, 1, 0>(sm, l);
     lds_fence();
     t_block<DK, B, 2, 0>(sm, l);
@@ -700,11 +712,11 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l) {
 
 // Wave 3, chunk x: K K^T below the diagonal into A, then T_32, T_21, T_31.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l) {
+__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     // K[B] staged; A (one buffer) was read by T's blocks of chunk x - 1
-    wait_all<2>({&sm.sync.staged, &sm.sync.tfull}, {4 * (x + 1), 2 * x});
+    wait_all<2>(lim, {&sm.sync.staged, &sm.sync.tfull}, {4 * (x + 1), 2 * x});
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
@@ -715,7 +727,7 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l) {
     kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l);
     kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l);
     signal(&sm.sync.aoff);
-    wait_ge(&sm.sync.tdiag, x + 1);
+    wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
     t_block<DK, B, 2, 1>(sm, l);
     lds_fence();
@@ -769,13 +781,13 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
                                             const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
     // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
     Sync& sy = sm.sync;
-    wait_all<5>({&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
+    wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
                 {x - 1, x - 1, 4 * (x - 1), x - 1, x - 1});
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
     stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
     signal(&sm.sync.staged);
     if (x + 2 < u.nch) load_chunk_any<DK>(p, u, x + 2, lo, lt, in);
-    wait_ge(&sm.sync.staged, 4 * (x + 1));
+    wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
     qk_blocks<DK, B, LW>(sm, lt & 63);
     signal(&sm.sync.pdone);
 }
@@ -826,7 +838,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
     f32x4 OQ[4];
     f16x8 Br[2];
     int er = 0;
-    wait_ge(&sm.sync.staged, 4 * (c + 1));
+    wait_ge(p.spin_limit, &sm.sync.staged, 4 * (c + 1));
     {
         // Operands of this interval, read ahead of their products.
         f16x8 kx[4][NK];
@@ -920,7 +932,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         for (int tb2 = 0; tb2 < 4; ++tb2) OQ[tb2] *= gq[tb2] * fo;
     }
     // ---- U = T Rhat, O^T += U^T P^T, S update.
-    wait_all<2>({&sm.sync.tfull, &sm.sync.pdone}, {2 * (c + 1), 4 * (c + 1)});
+    wait_all<2>(p.spin_limit, {&sm.sync.tfull, &sm.sync.pdone}, {2 * (c + 1), 4 * (c + 1)});
     {
         const int F1 = st.F + er;
         // T rows (both 32-token halves for rows >= 32), P rows, decays.
@@ -1084,13 +1096,13 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         }
     } else if (w == 2) {
         for (int x = 0; x < u.nch; x += 2) {
-            prep_wave2<DK, 0>(sm, x, l);
-            if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l);
+            prep_wave2<DK, 0>(sm, x, l, p.spin_limit);
+            if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l, p.spin_limit);
         }
     } else if (w == 3) {
         for (int x = 0; x < u.nch; x += 2) {
-            prep_wave3<DK, 0>(sm, x, l);
-            if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l);
+            prep_wave3<DK, 0>(sm, x, l, p.spin_limit);
+            if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l, p.spin_limit);
         }
     } else if (w == 4) {
         loader_loop<DK, 0>(p, sm, u, tid - 256);
@@ -1119,7 +1131,15 @@ size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a) {
     return a.cu_seqlens ? ((sizeof(int) * (size_t)a.batch + 255) & ~size_t(255)) : 0;
 }
 
-hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st) {
+hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
+    hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_sync_timeouts), sizeof(unsigned int), 0,
+                                       hipMemcpyDeviceToHost);
+    if (e != hipSuccess || !reset) return e;
+    const unsigned int zero = 0;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_sync_timeouts), &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+}
+
+hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit) {
     ChunkParams cp;
     cp.q = static_cast<const uint16_t*>(a.q);
     cp.k = static_cast<const uint16_t*>(a.k);
@@ -1137,6 +1157,7 @@ hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st) {
     cp.d_v = a.d_v;
     cp.gate_is_alpha = a.gate_kind == RHZ_GATE_ALPHA;
     cp.n_tiles = (a.d_v + kTV - 1) / kTV;
+    cp.spin_limit = spin_limit > 0 ? spin_limit : kSpinLimit;
     cp.order = nullptr;
     if (a.cu_seqlens) {
         int* order = static_cast<int*>(a.workspace);

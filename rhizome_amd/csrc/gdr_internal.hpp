@@ -25,7 +25,12 @@ hipError_t launch_multistep(const rhz_gdr_multistep_args& a, hipStream_t stream)
 // d_k <= 128, d_v % 8 == 0 and 16-byte aligned tensors.
 bool chunked_supported(int d_k, int d_v);
 size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a);
-hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream);
+// spin_limit: polls after which an LDS wait gives up; <= 0 for the built-in
+// limit (tests pass a tiny one to force give-ups).
+hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream, int spin_limit = 0);
+// Reads (and with `reset`, zeroes) the current device's count of chunked-kernel
+// LDS waits that gave up.  Synchronous with respect to the device.
+hipError_t chunked_sync_timeouts(unsigned int* count, bool reset);
 
 // Local-block prologue and epilogue (gdr_aux.hip).
 hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t stream);

@@ -46,6 +46,14 @@ __device__ __forceinline__ double philox_normal(uint64_t seed, uint64_t stream, 
     return sqrt(-2.0 * log(u1)) * cos(6.28318530717958647692528676655900577 * u2);
 }
 
+// rng.rs:78-82 on u32 words 2e and 2e + 1 of the stream: next_f64 #e.
+__device__ __forceinline__ double philox_uniform(uint64_t seed, uint64_t stream, uint64_t e) {
+    uint32_t b[4];
+    philox_block(seed, stream, e >> 1, b);
+    const uint32_t w0 = (e & 1) ? b[2] : b[0], w1 = (e & 1) ? b[3] : b[1];
+    return double((uint64_t(w0 >> 5) << 26) | uint64_t(w1 >> 6)) / 9007199254740992.0;
+}
+
 __device__ __forceinline__ double sigmoid_f64(double x) {
     if (x >= 0.0) return 1.0 / (1.0 + exp(-x));
     const double e = exp(x);
@@ -69,6 +77,10 @@ __global__ __launch_bounds__(256) void philox_fill_kernel(int kind, uint64_t see
                                                           int dtype, void* out) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= count) return;
+    if (kind == RHZ_FILL_UNIFORM) {
+        put(out, dtype, i, philox_uniform(seed, sid, uint64_t(i)));
+        return;
+    }
     const double z = philox_normal(seed, sid, uint64_t(i));
     const double x = (mean == 0.0 && sd == 1.0) ? z : mean + sd * z;
     double y = x;

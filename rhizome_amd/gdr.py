@@ -12,7 +12,7 @@ crates/ops/src/delta.rs:63).
 """
 from __future__ import annotations
 
-from ctypes import byref, c_size_t
+from ctypes import byref, c_size_t, c_uint32
 
 import torch
 
@@ -121,6 +121,15 @@ def prefill(q, k, v, g=None, beta=None, *, alpha=None, cu_seqlens=None, initial_
         args.workspace, args.workspace_bytes = _ptr(workspace), workspace.numel()
     _abi.check(_abi.lib().rhz_gdr_prefill(byref(args), _stream(stream)))
     return o, fin
+
+
+def sync_timeouts(reset: bool = True) -> int:
+    """Number of the chunked kernel's LDS waits that gave up on the current
+    device since the last reset (0 unless a launch may have gone wrong).
+    Blocks until the device's outstanding work is done."""
+    n = c_uint32(0)
+    _abi.check(_abi.lib().rhz_gdr_sync_timeouts(byref(n), 1 if reset else 0))
+    return n.value
 
 
 def decode_args(q, k, v, gate, beta, gate_kind, state, o) -> _abi.DecodeArgs:
@@ -248,7 +257,8 @@ def rmsnorm_heads(x, scale, eps: float = 1e-6, *, out=None, stream=None):
 
 
 _FILL = {"normal": _abi.FILL_NORMAL, "unit_rows": _abi.FILL_UNIT_ROWS,
-         "sigmoid": _abi.FILL_SIGMOID, "neg_softplus": _abi.FILL_NEG_SOFTPLUS}
+         "sigmoid": _abi.FILL_SIGMOID, "neg_softplus": _abi.FILL_NEG_SOFTPLUS,
+         "uniform": _abi.FILL_UNIFORM}
 _FILL_DTYPES = {torch.float64: _abi.F64, torch.float32: _abi.F32, torch.bfloat16: _abi.BF16}
 
 

@@ -27,6 +27,11 @@ def _rng(seed):
     ([100, 100], 300, False),             # dense-shaped pack
     ([0, 1, 2, 3, 31, 32, 33, 0, 200], 257, True),   # empty and short sequences, span edges
     ([4096], 2048, True),
+    # empty and short sequences at a vectorized width (16-byte rows): every
+    # channel of an empty sequence must get its final state
+    ([0, 5, 0, 17, 1, 0], 2048, True),
+    ([0, 5, 0, 17, 1, 0], 2048, False),
+    ([0, 0, 0], 6144, True),              # zero tokens, final states only
 ])
 def test_conv1d(device, dtype, tol, lengths, C, with_state):
     rng = _rng(len(lengths) + C)

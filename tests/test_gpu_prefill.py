@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 import torch
 
-from gdr_cases import BF16_TOL, C0, C1, C2, C4, F32_TOL, Prefill, check_close, varlen_lengths
+from gdr_cases import (BF16_TOL, C0, C1, C2, C4, F32_TOL, Prefill, check_close, check_close_dev,
+                        nonexpansive_bound, varlen_lengths)
 
 pytestmark = pytest.mark.gpu
 
@@ -159,21 +160,59 @@ def test_config1_full(device, algo, dtype, tol):
     _check(w, o, fin, tol, tag=f"c1 {algo}")
 
 
+def _recurrent_fp32(w):
+    """The fp32 recurrent kernel (held to the oracle at 1e-4 on configs 0 and
+    1) on the chunked run's bf16 inputs widened exactly to fp32."""
+    import rhizome_amd
+    o, fin = rhizome_amd.prefill(w.shaped(w.q).float(), w.shaped(w.k).float(), w.shaped(w.v).float(),
+                                 w.shaped(w.g), w.shaped(w.beta), cu_seqlens=w.cu_dev,
+                                 initial_state=w.init, algo="recurrent")
+    torch.cuda.synchronize()
+    return o.reshape(w.n_tok, w.heads, w.d_v), fin
+
+
+def _check_all_units(w, o, fin, tag):
+    """Every (sequence, head) of a large workload: finite, within the bf16
+    tolerance of the fp32 recurrent kernel, and within the closed-form norm
+    bound; a subset is then checked against the f64 oracle directly."""
+    assert bool(torch.isfinite(o.float()).all()) and bool(torch.isfinite(fin).all()), f"{tag}: non-finite"
+    ro, rf = _recurrent_fp32(w)
+    # o by head: [H, tokens, d_v]
+    mo = check_close_dev(o.transpose(0, 1).contiguous(), ro.transpose(0, 1).contiguous(), BF16_TOL,
+                         f"{tag} o vs recurrent fp32", units=w.heads)
+    mf = check_close_dev(fin, rf, BF16_TOL, f"{tag} final state vs recurrent fp32",
+                         units=w.n_seqs * w.heads)
+    nonexpansive_bound(w, fin)
+    print(f"{tag} all {w.n_seqs * w.heads} units vs recurrent fp32: o {mo}  final {mf}", flush=True)
+    return ro, rf
+
+
 def test_config2_long_context(device):
-    """B=1 H=32 T=32768 d_k=128 d_v=256, slow decay; heads 0, 13 and 31 against the oracle."""
+    """B=1 H=32 T=32768 d_k=128 d_v=256, slow decay.  All 32 heads against the
+    fp32 recurrent kernel and the norm bound; heads 0, 13 and 31 of both
+    kernels against the f64 oracle."""
     w = Prefill(**C2, dtype=torch.bfloat16, device=device)
     o, fin = w.run(algo="chunked")
-    _check(w, o, fin, BF16_TOL, seqs=[0], heads=[0, 13, 31], tag="c2 chunked")
+    ro, rf = _check_all_units(w, o, fin, "c2 chunked")
+    heads = [0, 13, 31]
+    _check(w, o, fin, BF16_TOL, seqs=[0], heads=heads, tag="c2 chunked")
+    _check(w, ro, rf, F32_TOL, seqs=[0], heads=heads, tag="c2 recurrent fp32")
 
 
 def test_config4_varlen(device):
-    """64 packed sequences, lengths U[128, 8192], init states; 24 (seq, head) units checked."""
+    """64 packed sequences, lengths U[128, 8192], init states.  All 1024
+    (sequence, head) units against the fp32 recurrent kernel and the norm
+    bound; 4 sequences x 3 heads = 12 units of both kernels against the f64
+    oracle."""
     lengths = varlen_lengths(C4["n_seqs"], C4["len_lo"], C4["len_hi"])
     w = Prefill(heads=C4["heads"], d_k=C4["d_k"], d_v=C4["d_v"], lengths=lengths,
                 dtype=torch.bfloat16, device=device, state_std=C4["state_std"])
     o, fin = w.run(algo="chunked")
+    ro, rf = _check_all_units(w, o, fin, "c4 chunked")
     longest = int(np.argmax(lengths))
-    _check(w, o, fin, BF16_TOL, seqs=[0, 7, longest, 63], heads=[0, 5, 15], tag="c4 chunked")
+    seqs, heads = [0, 7, longest, 63], [0, 5, 15]
+    _check(w, o, fin, BF16_TOL, seqs=seqs, heads=heads, tag="c4 chunked")
+    _check(w, ro, rf, F32_TOL, seqs=seqs, heads=heads, tag="c4 recurrent fp32")
 
 
 @pytest.mark.parametrize("algo,dtype", [("chunked", torch.bfloat16), ("recurrent", torch.float32)])

@@ -17,9 +17,9 @@ HEADER = os.path.join(ROOT, "include", "rhizome_gdr.h")
 DOC = os.path.join(ROOT, "INTEGRATION.md")
 
 # C type (const, base, pointer depth) -> Rust type in sys.rs
-SCALARS = {"int32_t": "i32", "int64_t": "i64", "uint64_t": "u64", "size_t": "usize", "float": "f32",
+SCALARS = {"int32_t": "i32", "uint32_t": "u32", "int64_t": "i64", "uint64_t": "u64", "size_t": "usize", "float": "f32",
            "double": "f64", "rhz_status": "i32"}
-POINTEES = {"void": "c_void", "char": "c_char", "int32_t": "i32", "float": "f32", "size_t": "usize"}
+POINTEES = {"void": "c_void", "char": "c_char", "int32_t": "i32", "uint32_t": "u32", "float": "f32", "size_t": "usize"}
 
 
 def c_to_rust(ctype):
@@ -110,7 +110,7 @@ def both():
 def test_header_parses(both):
     (consts, structs, funcs), _ = both
     # guards the parser itself: everything the header declares was found
-    assert len(structs) == 6 and len(funcs) == 12 and consts["RHZ_ERR_HIP"] == 4
+    assert len(structs) == 6 and len(funcs) == 14 and consts["RHZ_ERR_HIP"] == 4
 
 
 def test_every_constant(both):
