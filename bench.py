@@ -132,12 +132,20 @@ def multistep_bytes(batch, heads, dk, dv, n) -> float:
 SETTLE_MS = 150.0  # wall time of untimed launches before each leg's counted warmup
 
 
-def settle(torch, fn, ms: float = SETTLE_MS) -> dict:
-    """Runs fn back to back for at least `ms` of wall time before anything is
-    counted.  The GPU's clocks ramp up over the first tens of milliseconds of
-    sustained work; without this, a short counted warmup leaves the timed
-    launches on a rising clock.  Nothing here is timed or reported as a
-    result: the JSON line only records how long the settle phase ran."""
+def set_settle_ms(ms: float) -> None:
+    global SETTLE_MS
+    SETTLE_MS = float(ms)
+
+
+def settle(torch, fn, frac: float = 1.0) -> dict:
+    """Runs fn back to back for at least frac * SETTLE_MS of wall time before
+    anything is counted.  The GPU's clocks ramp up over the first tens of
+    milliseconds of sustained work; without this, a short counted warmup
+    leaves the timed launches on a rising clock.  Nothing here is timed or
+    reported as a result: the JSON line records how long the settle phase ran
+    and how many launches it made (so that a kernel trace of the run can be
+    split into each leg's settle, warmup and timed launches)."""
+    ms = SETTLE_MS * frac
     t0 = time.perf_counter()
     n = 0
     while (time.perf_counter() - t0) * 1e3 < ms:
@@ -231,7 +239,8 @@ def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
         cfg.update(n_seqs=len(c["lengths"]), tokens=host["tokens"], min_len=min(c["lengths"]),
                    max_len=max(c["lengths"]))
     return {"metric": "GDR prefill tokens/s", "value": host["tokens"] / (ms * 1e-3), "unit": "tokens/s",
-            "ms_per_step": ms, "steps": steps, "settle_ms": host["settle_ms"],
+            "ms_per_step": ms, "steps": steps, "warmup": warmup, "settle_ms": host["settle_ms"],
+            "settle_launches": host["settle_launches"],
             "config": {"workload": workload, **cfg},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles(profile_key),
@@ -300,11 +309,11 @@ def bench_multistep(torch, steps, warmup):
         if st:
             _abi.check(st)
 
-    settle(torch, step, SETTLE_MS / 3)
+    info = settle(torch, step, 1 / 3)
     for _ in range(warmup):
         step()
     ms = time_region(torch, stream, step, steps)
-    return ms, multistep_bytes(B, H, dk, dv, n)
+    return ms, multistep_bytes(B, H, dk, dv, n), info
 
 
 def bench_aux(torch, steps, warmup):
@@ -340,12 +349,13 @@ def bench_aux(torch, steps, warmup):
     }
     out = {}
     for name, (fn, nbytes, kernel, shape) in jobs.items():
-        settle(torch, fn, SETTLE_MS / 3)
+        info = settle(torch, fn, 1 / 3)
         for _ in range(warmup):
             fn()
         ms = time_region(torch, stream, fn, steps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"value": gbs, "unit": "GB/s", "ms_per_step": ms, "workload": shape,
+                     "steps": steps, "warmup": warmup, **info,
                      "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
                                   "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles(name),
                                   "kernel": kernel, "bytes_per_launch": float(nbytes),
@@ -438,6 +448,8 @@ def main() -> int:
     # counted warmup, then the timed steps
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed launches before each leg's warmup, in ms of wall time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy", action="store_true")
     args = ap.parse_args()
@@ -452,10 +464,11 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    set_settle_ms(args.settle_ms)
     ms, flops, algo_bytes, pre_host = bench_prefill(torch, args.steps, args.warmup)
     dms, dbytes, dec_host = bench_decode(torch, args.warmup)
-    dlms, dlbytes, _ = bench_decode(torch, min(args.warmup, 16), DECODE_LARGE)
-    mms, mbytes = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
+    dlms, dlbytes, dl_host = bench_decode(torch, min(args.warmup, 16), DECODE_LARGE)
+    mms, mbytes, ms_info = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
     aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
     long_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), PREFILL_LONG,
                            "chunked GDR prefill, long context, slow decay", "prefill_long")
@@ -510,7 +523,8 @@ def main() -> int:
                                 "traffic": traffic_from_profiles("decode"),
                                 "kernel": "gdr_decode_kernel<8,4,true,float>",
                                 "bytes_per_launch": dbytes, "launch_us": dms * 1e3},
-                   "settle_ms": dec_host["settle_ms"]},
+                   "warmup": args.warmup, "settle_ms": dec_host["settle_ms"],
+                   "settle_launches": dec_host["settle_launches"]},
         # control: the same step with the state 4x the 256 MB last-level
         # cache, so that the decode rate above is not a cache effect
         "decode_large_state": {
@@ -522,7 +536,8 @@ def main() -> int:
                          "unit": "GB/s", "frac": dlbytes / (dlms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          "traffic": traffic_from_profiles("decode_large"),
                          "kernel": "gdr_decode_kernel<8,4,true,float>", "bytes_per_launch": dlbytes,
-                         "launch_us": dlms * 1e3}},
+                         "launch_us": dlms * 1e3},
+            "warmup": min(args.warmup, 16), "settle_launches": dl_host["settle_launches"]},
         "prefill_long_context": long_leg,
         "prefill_varlen": varlen_leg,
         "multistep": {"metric": "multistep HBM GB/s (state read, per-position snapshots written)",
@@ -534,7 +549,8 @@ def main() -> int:
                                    "frac": mbytes / (mms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                    "traffic": traffic_from_profiles("multistep"),
                                    "kernel": "gdr_multistep_kernel<8,2,true,float>",
-                                   "bytes_per_launch": mbytes, "launch_us": mms * 1e3}},
+                                   "bytes_per_launch": mbytes, "launch_us": mms * 1e3},
+                      "steps": min(args.steps, 50), "warmup": min(args.warmup, 20), **ms_info},
         "prologue_epilogue": aux,
         "device": device_info(torch),
     }
