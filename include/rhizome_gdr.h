@@ -179,6 +179,24 @@ rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size
 /* Gated delta-rule prefill (see rhz_gdr_prefill_args). */
 rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream);
 
+/* rhz_gdr_prefill for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  It has no counterpart in the reference.  Same arguments,
+ * validation and results as rhz_gdr_prefill, except that `workspace` and
+ * `workspace_bytes` are ignored: the only scratch of the prefill (a packed
+ * batch's sequence order, 4 bytes per sequence) lives in a static device
+ * array of RHZ_NOALLOC_MAX_SEQS entries (256 KiB) that each GPU the library
+ * runs on holds until the process ends.  A packed batch of more than
+ * RHZ_NOALLOC_MAX_SEQS sequences is rejected with RHZ_ERR_UNSUPPORTED.  The
+ * first call on a device looks up that device's copy of the array; no call
+ * allocates.  Every call on one GPU shares the array: calls that overlap on
+ * one GPU (on different streams, or from threads without ordering) race on
+ * it and must be serialised by the caller; a race gives wrong results, not
+ * accesses outside the caller's buffers. */
+#define RHZ_NOALLOC_MAX_SEQS 65536
+
+rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* stream);
+
 /* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
  * reference, whose op is a CPU loop).  The kernel's waves synchronise through
  * LDS counters with bounded waits; a wait that gives up lets the kernel end

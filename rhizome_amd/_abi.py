@@ -28,6 +28,7 @@ ALGO_AUTO, ALGO_RECURRENT, ALGO_CHUNKED = 0, 1, 2
 # rhz_op
 OP_DELTA_SCAN, OP_DELTA_STEP, OP_DELTA_MULTISTEP = 0, 1, 2
 MULTISTEP_MAX = 64
+NOALLOC_MAX_SEQS = 65536
 # rhz_fill_kind
 FILL_NORMAL, FILL_UNIT_ROWS, FILL_SIGMOID, FILL_NEG_SOFTPLUS, FILL_UNIFORM = 0, 1, 2, 3, 4
 
@@ -122,6 +123,8 @@ def lib():
         L.rhz_gdr_prefill_workspace_size.restype = c_int32
         L.rhz_gdr_prefill.argtypes = [POINTER(PrefillArgs), c_void_p]
         L.rhz_gdr_prefill.restype = c_int32
+        L.rhz_gdr_prefill_noalloc.argtypes = [POINTER(PrefillArgs), c_void_p]
+        L.rhz_gdr_prefill_noalloc.restype = c_int32
         L.rhz_gdr_sync_timeouts.argtypes = [POINTER(c_uint32), c_int32]
         L.rhz_gdr_sync_timeouts.restype = c_int32
         L.rhz_gdr_prefill_spin_limit.argtypes = [POINTER(PrefillArgs), c_int32, c_void_p]

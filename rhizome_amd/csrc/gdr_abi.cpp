@@ -174,6 +174,21 @@ rhz_status rhz_gdr_prefill_spin_limit(const rhz_gdr_prefill_args* args, int32_t 
     return prefill_impl(args, stream, spin_limit);
 }
 
+rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* stream) {
+    int algo = 0;
+    const rhz_status s = check_prefill(args, true, &algo);
+    if (s != RHZ_OK) return s;
+    if (args->seq_len == 0 && !args->final_state) return ok();
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (algo == RHZ_ALGO_CHUNKED) {
+        if (args->cu_seqlens && args->batch > RHZ_NOALLOC_MAX_SEQS)
+            return fail(RHZ_ERR_UNSUPPORTED, "rhz_gdr_prefill_noalloc takes at most %d packed sequences (got %d)",
+                        RHZ_NOALLOC_MAX_SEQS, args->batch);
+        return hip_status(rhz::launch_chunked_noalloc(*args, st), "chunked prefill launch (no allocation)");
+    }
+    return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");
+}
+
 rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset) {
     if (!count) return fail(RHZ_ERR_INVALID_ARG, "count is NULL");
     unsigned int n = 0;

@@ -57,6 +57,7 @@
 // U) far from overflow and underflow, so in steady state no rescaling
 // multiply is executed, and every scale change is exact.
 
+#include <mutex>
 #include <utility>
 
 #include "gdr_device.hpp"
@@ -1041,7 +1042,9 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     const int seqi = unit / H;
     Unit u;
     u.h = unit - seqi * H;
-    u.seq = p.order ? p.order[seqi] : seqi;
+    // (clamped: an order buffer that another call overwrote gives wrong
+    // results, never an access outside this call's sequences)
+    u.seq = p.order ? min(max(p.order[seqi], 0), p.batch - 1) : seqi;
     seq_bounds(p.cu_seqlens, u.seq, p.seq_len, u.tb, u.te);
     u.nch = (u.te - u.tb + kChunk - 1) / kChunk;
     u.i0 = tile * kTV;
@@ -1139,7 +1142,61 @@ hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
     return hipMemcpyToSymbol(HIP_SYMBOL(g_sync_timeouts), &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
 }
 
+namespace {
+
+// The scratch of rhz_gdr_prefill_noalloc: the longest-first order of up to
+// kNoAllocMaxSeqs packed sequences (256 KiB).  Each GPU holds its own copy
+// until the process ends, and every call on that GPU shares it.  Host code
+// never uses this name as an address: the device address of each GPU's copy
+// is looked up once (hipGetSymbolAddress, with that device current) and kept
+// in g_scratch_dev.
+__device__ __align__(256) int scratch[kNoAllocMaxSeqs];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int* g_scratch_dev[kMaxDevices] = {};  // written under g_scratch_mu
+
+// Device address of the current device's scratch (looked up on the first
+// call on that device).
+hipError_t noalloc_scratch(int** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_dev[dev] = static_cast<int*>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+
+// The chunked launch with the packed-batch order in `order_buf` (room for
+// a.batch ints; unused for dense batches).
+hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf);
+
+}  // namespace
+
 hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit) {
+    return launch_chunked_with(a, st, spin_limit, static_cast<int*>(a.workspace));
+}
+
+hipError_t launch_chunked_noalloc(const rhz_gdr_prefill_args& a, hipStream_t st) {
+    int* order_buf = nullptr;
+    if (a.cu_seqlens) {
+        if (a.batch > kNoAllocMaxSeqs) return hipErrorInvalidValue;  // the ABI rejects this first
+        const hipError_t e = noalloc_scratch(&order_buf);
+        if (e != hipSuccess) return e;
+    }
+    return launch_chunked_with(a, st, 0, order_buf);
+}
+
+namespace {
+hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf) {
     ChunkParams cp;
     cp.q = static_cast<const uint16_t*>(a.q);
     cp.k = static_cast<const uint16_t*>(a.k);
@@ -1160,17 +1217,17 @@ hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st, int spi
     cp.spin_limit = spin_limit > 0 ? spin_limit : kSpinLimit;
     cp.order = nullptr;
     if (a.cu_seqlens) {
-        int* order = static_cast<int*>(a.workspace);
         hipLaunchKernelGGL(gdr_varlen_order_kernel, dim3(1), dim3(1024), 0, st, a.cu_seqlens, a.batch, a.seq_len,
-                           order);
+                           order_buf);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        cp.order = order;
+        cp.order = order_buf;
     }
     const int blocks = a.batch * a.heads * cp.n_tiles;
     if (a.d_k <= 32) return chunked_go<32>(cp, blocks, st);
     if (a.d_k <= 64) return chunked_go<64>(cp, blocks, st);
     return chunked_go<128>(cp, blocks, st);
 }
+}  // namespace
 
 }  // namespace rhz

@@ -28,6 +28,12 @@ size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a);
 // spin_limit: polls after which an LDS wait gives up; <= 0 for the built-in
 // limit (tests pass a tiny one to force give-ups).
 hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream, int spin_limit = 0);
+// The chunked launch of rhz_gdr_prefill_noalloc: the packed-batch order
+// lives in a static device array of kNoAllocMaxSeqs ints (a.workspace is
+// not used); the caller has checked a.batch <= kNoAllocMaxSeqs for packed
+// batches.
+constexpr int kNoAllocMaxSeqs = RHZ_NOALLOC_MAX_SEQS;
+hipError_t launch_chunked_noalloc(const rhz_gdr_prefill_args& a, hipStream_t stream);
 // Reads (and with `reset`, zeroes) the current device's count of chunked-kernel
 // LDS waits that gave up.  Synchronous with respect to the device.
 hipError_t chunked_sync_timeouts(unsigned int* count, bool reset);

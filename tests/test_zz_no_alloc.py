@@ -1,0 +1,69 @@
+"""rhz_gdr_prefill_noalloc: the prefill entry point that allocates nothing.
+
+Its only scratch (a packed batch's longest-first sequence order) is a static
+device array shared by every call on a GPU, so two calls in a row -- the
+second with fewer sequences -- must each match rhz_gdr_prefill (same kernels,
+caller-provided workspace) bit for bit.  A dense batch and the fp32
+recurrent path, which use no scratch, must match too.  The size limit is
+checked before any HIP call.
+"""
+from ctypes import byref
+
+import pytest
+import torch
+
+import rhizome_amd
+from gdr_cases import Prefill
+from rhizome_amd import _abi, gdr
+
+
+def _noalloc(w, algo):
+    """rhz_gdr_prefill_noalloc through the C ABI on workload w."""
+    o = torch.empty_like(w.shaped(w.v))
+    fin = torch.empty((w.n_seqs, w.heads, w.d_v, w.d_k), dtype=torch.float32, device=w.q.device)
+    args = gdr.prefill_args(w.shaped(w.q), w.shaped(w.k), w.shaped(w.v), w.shaped(w.g), w.shaped(w.beta),
+                            _abi.GATE_LOG_ALPHA, w.cu_dev, w.init, fin, o, algo)
+    stream = torch.cuda.current_stream().cuda_stream or None
+    _abi.check(_abi.lib().rhz_gdr_prefill_noalloc(byref(args), stream))
+    torch.cuda.synchronize()
+    assert rhizome_amd.sync_timeouts() == 0
+    return o.reshape(w.n_tok, w.heads, w.d_v), fin
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_prefill_two_calls(device):
+    # first call: 40 packed sequences; second: 5 (the shared scratch keeps the
+    # first call's order beyond entry 5)
+    for n_seqs, seed in ((40, 0), (5, 1)):
+        lengths = [int(x) for x in torch.randint(0, 300, (n_seqs,), generator=torch.Generator().manual_seed(seed))]
+        lengths[0] = 0
+        w = Prefill(heads=3, d_k=128, d_v=128, lengths=lengths, seed=seed, dtype=torch.bfloat16,
+                    device=device, state_std=0.02)
+        o1, f1 = _noalloc(w, "chunked")
+        o2, f2 = w.run(algo="chunked")  # rhz_gdr_prefill with its own workspace
+        assert torch.equal(o1, o2) and torch.equal(f1, f2), f"{n_seqs} sequences"
+        print(f"noalloc == prefill, {n_seqs} packed sequences, {w.n_tok} tokens", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("algo,dtype", [("chunked", torch.bfloat16), ("recurrent", torch.float32)])
+def test_noalloc_dense_and_recurrent(device, algo, dtype):
+    w = Prefill(batch=2, heads=2, seq_len=150, d_k=64, d_v=64, dtype=dtype, device=device, state_std=0.02)
+    o1, f1 = _noalloc(w, algo)
+    o2, f2 = w.run(algo=algo)
+    assert torch.equal(o1, o2) and torch.equal(f1, f2)
+
+
+def _gpu_visible() -> bool:
+    return torch.cuda.device_count() > 0
+
+
+@pytest.mark.skipif(_gpu_visible(), reason="fake device addresses: CPU-only validation test")
+def test_noalloc_rejects_more_sequences_than_its_scratch():
+    A = 0x10000  # aligned fake address: the call must stop before any HIP call
+    a = _abi.PrefillArgs()
+    a.batch, a.seq_len, a.heads, a.d_k, a.d_v, a.chunk = _abi.NOALLOC_MAX_SEQS + 1, 100, 1, 128, 128, 64
+    a.dtype, a.gate_kind, a.algo = _abi.BF16, _abi.GATE_LOG_ALPHA, _abi.ALGO_CHUNKED
+    a.q = a.k = a.v = a.gate = a.beta = a.o = a.cu_seqlens = A
+    assert _abi.lib().rhz_gdr_prefill_noalloc(byref(a), None) == _abi.ERR_UNSUPPORTED
+    assert "at most" in _abi.last_error()
