@@ -21,7 +21,8 @@ from ctypes import POINTER, c_double, c_int, c_int64, c_uint32, c_uint64, c_void
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# RHIZOME_ORACLE_LIB names another build of the oracle (the sanitizer build)
+_LIB_PATH = os.environ.get("RHIZOME_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 _dp = POINTER(c_double)

@@ -14,7 +14,9 @@ from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int32, c_
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "librhizome_gdr.so")
+# RHIZOME_GDR_LIB names another build of the same library (the host
+# sanitizer build under _build/asan, for example); there is no other backend.
+LIB_PATH = os.environ.get("RHIZOME_GDR_LIB") or os.path.join(HERE, "librhizome_gdr.so")
 HEADER = os.path.join(ROOT, "include", "rhizome_gdr.h")
 
 # rhz_status

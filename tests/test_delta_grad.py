@@ -10,7 +10,8 @@ a reset cuts every earlier gradient to zero, d g = d alpha * alpha.
 import os
 import subprocess
 
-BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_delta_grad")
+BIN = os.path.join(os.environ.get("RHIZOME_TEST_BIN_DIR") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                        "cpp"), "test_delta_grad")
 
 
 def test_adjoint_gradcheck():

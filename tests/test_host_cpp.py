@@ -8,7 +8,8 @@ import subprocess
 
 import pytest
 
-BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_delta_host")
+BIN = os.path.join(os.environ.get("RHIZOME_TEST_BIN_DIR") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                        "cpp"), "test_delta_host")
 
 
 def _run(*args):

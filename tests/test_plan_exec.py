@@ -19,7 +19,8 @@ import pytest
 
 from oracle import plan_oracle as P
 
-BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_plan_exec")
+BIN = os.path.join(os.environ.get("RHIZOME_TEST_BIN_DIR") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                        "cpp"), "test_plan_exec")
 
 
 def _run(*args):
