@@ -431,18 +431,23 @@ __device__ __forceinline__ void load_chunk(const ChunkParams& p, const Unit& u, 
     r.bv = *reinterpret_cast<const float*>(bb + o.bv);
 }
 
-// Loads chunk c; the offsets of a partial last chunk are clamped.
+// Loads chunk min(c, nch - 1) (past the end the loads repeat the last chunk
+// and are not used).  Only the last chunk can be partial: its offsets,
+// clamped to its last token, are selected without a branch, so that the
+// compiler's wait for one register set never waits for the loads of the
+// other.
 template <int DK>
 __device__ __forceinline__ void load_chunk_any(const ChunkParams& p, const Unit& u, int c, const LoadOffsets<DK>& full,
-                                               int lt, ChunkIn<DK>& r) {
-    const int len = min(kChunk, u.te - (u.tb + c * kChunk));
-    if (len == kChunk) {
-        load_chunk<DK>(p, u, c, full, r);
-    } else {
-        LoadOffsets<DK> o;
-        o.set(p, u.i0, lt, len - 1);
-        load_chunk<DK>(p, u, c, o, r);
-    }
+                                               const LoadOffsets<DK>& lastc, ChunkIn<DK>& r) {
+    c = min(c, u.nch - 1);
+    const bool is_last = c == u.nch - 1;  // uniform
+    LoadOffsets<DK> o;
+#pragma unroll
+    for (int i = 0; i < DK / 32; ++i) o.kq[i] = is_last ? lastc.kq[i] : full.kq[i];
+    o.v = is_last ? lastc.v : full.v;
+    o.g = is_last ? lastc.g : full.g;
+    o.bv = is_last ? lastc.bv : full.bv;
+    load_chunk<DK>(p, u, c, o, r);
 }
 
 template <int DK, int NB>
@@ -779,7 +784,8 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
 // two chunk periods to arrive.
 template <int DK, int B, int LW>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
-                                            const LoadOffsets<DK>& lo, ChunkIn<DK>& in) {
+                                            const LoadOffsets<DK>& lo, const LoadOffsets<DK>& lastc,
+                                            ChunkIn<DK>& in) {
     // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
     Sync& sy = sm.sync;
     wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
@@ -787,7 +793,7 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
     stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
     signal(&sm.sync.staged);
-    if (x + 2 < u.nch) load_chunk_any<DK>(p, u, x + 2, lo, lt, in);
+    load_chunk_any<DK>(p, u, x + 2, lo, lastc, in);
     wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
     qk_blocks<DK, B, LW>(sm, lt & 63);
     signal(&sm.sync.pdone);
@@ -795,14 +801,17 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
 
 template <int DK, int LW>
 __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int lt) {
-    LoadOffsets<DK> lo;
+    if (u.nch <= 0) return;
+    LoadOffsets<DK> lo, lastc;
     lo.set(p, u.i0, lt, kChunk - 1);
+    lastc.set(p, u.i0, lt, u.te - (u.tb + (u.nch - 1) * kChunk) - 1);
     ChunkIn<DK> in0, in1;
-    if (u.nch > 0) load_chunk_any<DK>(p, u, 0, lo, lt, in0);
-    if (u.nch > 1) load_chunk_any<DK>(p, u, 1, lo, lt, in1);
+    load_chunk_any<DK>(p, u, 0, lo, lastc, in0);
+    load_chunk_any<DK>(p, u, 1, lo, lastc, in1);
     for (int x = 0; x < u.nch; x += 2) {
-        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, in0);
-        if (x + 1 < u.nch) prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, in1);
+        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, lastc, in0);
+        if (x + 1 >= u.nch) break;
+        prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, lastc, in1);
     }
 }
 
