@@ -64,9 +64,15 @@ typedef enum rhz_gate { RHZ_GATE_LOG_ALPHA = 0, RHZ_GATE_ALPHA = 1 } rhz_gate;
  * CHUNKED:   64-token chunks, WY/UT transform on fp16 MFMA with fp32
  *            accumulation and fp32 state (bf16 inputs only, converted to
  *            fp16 on chip).  q and k are expected L2-normalised, as the
- *            reference's op takes them (delta.rs:17), so that every element
- *            lies within fp16's range; the state and intermediate products
- *            are rescaled by powers of two and have no such limit. */
+ *            reference's op takes them (delta.rs:17), so that their
+ *            elements and inner products lie within fp16's range
+ *            (|x| < 65520); the state and the corrected values U are
+ *            rescaled by powers of two and have no such limit.  Launches
+ *            that meet q, k or products beyond that range, or non-finite
+ *            q or k, are counted by rhz_gdr_fp16_range_errors: their
+ *            results are not to be trusted, and RECURRENT takes such
+ *            inputs.  A log-decay at or below -80 (alpha <= 1.8e-35) is
+ *            taken as alpha = 0: the past is forgotten exactly. */
 typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUNKED = 2 } rhz_algo;
 
 /* Op identities for rhz_gdr_query_support, named after the plan-level ops
@@ -205,6 +211,17 @@ rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* strea
  * device's outstanding work.  A nonzero count means that some chunked launch
  * since the last reset may have produced wrong results. */
 rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset);
+
+/* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
+ * reference, whose op computes in f32 throughout): the number of
+ * (workgroup, chunk, wave) steps since the last reset whose fp16 MFMA
+ * operands formed from q and k on chip -- the blocks of beta K K^T and
+ * Q K^T with their decays -- held a NaN, an infinity or a value of
+ * magnitude 65520 or more.  That happens for q or k elements or inner
+ * products beyond fp16's range and for non-finite q or k; a nonzero count
+ * means that some chunked launch since the last reset may have produced
+ * wrong results.  Same calling convention as rhz_gdr_sync_timeouts. */
+rhz_status rhz_gdr_fp16_range_errors(uint32_t* count, int32_t reset);
 
 /* Test hook (no counterpart in the reference): rhz_gdr_prefill with the
  * CHUNKED kernel's waits bounded at spin_limit polls (>= 1) instead of the

@@ -198,6 +198,15 @@ rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset) {
     return ok();
 }
 
+rhz_status rhz_gdr_fp16_range_errors(uint32_t* count, int32_t reset) {
+    if (!count) return fail(RHZ_ERR_INVALID_ARG, "count is NULL");
+    unsigned int n = 0;
+    const hipError_t e = rhz::chunked_range_errors(&n, reset != 0);
+    if (e != hipSuccess) return hip_status(e, "reading the fp16 range error count");
+    *count = n;
+    return ok();
+}
+
 }  // extern "C"
 
 namespace {

@@ -68,6 +68,12 @@ namespace {
 
 // Number of LDS waits that gave up since the last reset (per device).
 __device__ unsigned int g_sync_timeouts;
+// Number of (workgroup, wave) pairs since the last reset in which an fp16
+// entry of A or P (the MFMA operands formed from q and k) was NaN,
+// infinite or too large for fp16 (|x| >= 65520): q or k elements or their
+// inner products beyond fp16's range, or non-finite q or k.  The operands
+// formed from v and the state are rescaled by powers of two instead.
+__device__ unsigned int g_range_errors;
 
 constexpr int kTV = 32;           // rows of S per workgroup (two scan waves of 16)
 constexpr int kMaxSortSeqs = 4096;
@@ -230,6 +236,27 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xc, 0xf, false));
     return x;
 }
+// The same prefix sum restarted at segment boundaries: lane i sums x_j over
+// j <= i with seg_j == seg_i (seg non-decreasing over the lanes).  A lane's
+// partial sum covers only its own segment's part of its window, so at each
+// shift it takes over the source lane's partial sum only when the two lanes
+// are in one segment.  Sums of one segment never see values of another, so
+// they are the same numbers whatever came before the segment.
+template <int CTRL, int ROWS, bool BOUND>
+__device__ __forceinline__ float seg_step(float x, float seg) {
+    const float sx = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROWS, 0xf, BOUND));
+    const float ss = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, seg), CTRL, ROWS, 0xf, BOUND));
+    return x + (ss == seg ? sx : 0.f);
+}
+__device__ __forceinline__ float wave_seg_scan(float x, float seg) {
+    x = seg_step<0x111, 0xf, true>(x, seg);
+    x = seg_step<0x112, 0xf, true>(x, seg);
+    x = seg_step<0x114, 0xf, true>(x, seg);
+    x = seg_step<0x118, 0xf, true>(x, seg);
+    x = seg_step<0x142, 0xa, false>(x, seg);
+    x = seg_step<0x143, 0xc, false>(x, seg);
+    return x;
+}
 __device__ __forceinline__ float lane_val(float x, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }
@@ -351,6 +378,24 @@ __device__ __forceinline__ void wait_all(int lim, int* const (&c)[N], const int 
 }
 __device__ __forceinline__ void wait_ge(int lim, int* cnt, int target) { wait_all<1>(lim, {cnt}, {target}); }
 
+// Range watch over fp16 operands: both halves of rng keep the running
+// maximum of the magnitude bits (sign cleared) of the fp16 values seen, so
+// that a half at or above 0x7c00 means an infinity or a NaN -- a value that
+// was not finite, or that rounded to infinity (|x| >= 65520).  Two packed
+// 16-bit maxima and two ANDs per four values.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void range_watch(uint32_t& rng, uint2 h) {
+    const u16x2 a = __builtin_bit_cast(u16x2, h.x & 0x7fff7fffu);
+    const u16x2 b = __builtin_bit_cast(u16x2, h.y & 0x7fff7fffu);
+    rng = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, rng),
+                                                                 __builtin_elementwise_max(a, b)));
+}
+// One count in g_range_errors when any lane of the wave saw such a value.
+__device__ __forceinline__ void note_range(uint32_t rng) {
+    const bool bad = (rng & 0xffffu) >= 0x7c00u || (rng >> 16) >= 0x7c00u;
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicAdd(&g_range_errors, 1u);
+}
+
 // Shared memory of one workgroup.  Buffers indexed [2] are double-buffered
 // by chunk parity.  T and P hold zeros above the diagonal blocks for the
 // whole kernel.
@@ -371,6 +416,8 @@ struct Smem {
     float dst[2][64];                // exp(G_s - G_{16 floor(s/16)})
     float den[2][64];                // exp(G_{16 floor(s/16) + 15} - G_s)
     float pf[2][16];                 // [4 bi + bj]: exp(G_{16 bi} - G_{16 bj + 15}), bi > bj
+    float seg[2][64];                // segment of token s: resets at or before s
+    int resets[2];                   // the chunk has a reset (seg is then valid)
     Sync sync;
 };
 
@@ -450,31 +497,67 @@ __device__ __forceinline__ void load_chunk_any(const ChunkParams& p, const Unit&
     load_chunk<DK>(p, u, c, o, r);
 }
 
-template <int DK, int NB>
-__device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, int s, int len, const ChunkIn<DK>& r) {
-    const float g = s < len ? log_decay(r.g, p.gate_is_alpha) : 0.f;
-    const float beta = s < len ? r.b : 0.f;
-    const float G = wave_incl_scan(g);
+// The chunk's decay vectors, lane s = token s.  A reset token (is_reset)
+// starts a new segment: seg_s counts the resets at or before s, G_s sums
+// the log-decays of s's segment up to s (a reset token's own enters as 0),
+// and every factor that spans a reset is exactly zero -- exp(G_r - G_s)
+// stands for prod_{s < u <= r} alpha_u only where seg_r == seg_s, and
+// exp(G_s) for prod_{u <= s} alpha_u only where seg_s == 0.  Everything from
+// a reset on is then computed from the same numbers whatever came before
+// it.  Tokens past the chunk's end get g = 0 and beta = 0.
+template <int DK, int NB, bool SEG>
+__device__ __forceinline__ void stage_gates_as(Smem<DK>& sm, int s, float g, float beta, bool rst) {
+    const float sg = SEG ? wave_incl_scan(rst ? 1.f : 0.f) : 0.f;  // small integers: exact
+    const float G = SEG ? wave_seg_scan(g, sg) : wave_incl_scan(g);
     const float Glast = lane_val(G, 63);
     const float B0 = lane_val(G, 0), B1 = lane_val(G, 16), B2 = lane_val(G, 32), B3 = lane_val(G, 48);
     const float E0 = lane_val(G, 15), E1 = lane_val(G, 31), E2 = lane_val(G, 47);
     const int blk = s >> 4;
     const float Gs = blk == 0 ? B0 : blk == 1 ? B1 : blk == 2 ? B2 : B3;
     const float Ge = blk == 0 ? E0 : blk == 1 ? E1 : blk == 2 ? E2 : Glast;
-    const float gam = __expf(G);
+    float gam = __expf(G), gdl = __expf(Glast - G), dst = __expf(G - Gs), den = __expf(Ge - G);
+    float pf = 0.f;
+    const int bi = (s & 15) >> 2, bj = s & 3;
+    if (s < 16 && bi > bj) {
+        const float gi = bi == 1 ? B1 : bi == 2 ? B2 : B3;
+        const float gj = bj == 0 ? E0 : bj == 1 ? E1 : E2;
+        pf = __expf(gi - gj);
+    }
+    if constexpr (SEG) {
+        const float Slast = lane_val(sg, 63);
+        const float SB0 = lane_val(sg, 0), SB1 = lane_val(sg, 16), SB2 = lane_val(sg, 32), SB3 = lane_val(sg, 48);
+        const float SE0 = lane_val(sg, 15), SE1 = lane_val(sg, 31), SE2 = lane_val(sg, 47);
+        const float Ss = blk == 0 ? SB0 : blk == 1 ? SB1 : blk == 2 ? SB2 : SB3;
+        const float Se = blk == 0 ? SE0 : blk == 1 ? SE1 : blk == 2 ? SE2 : Slast;
+        gam = sg == 0.f ? gam : 0.f;
+        gdl = sg == Slast ? gdl : 0.f;
+        dst = sg == Ss ? dst : 0.f;
+        den = sg == Se ? den : 0.f;
+        const float si = bi == 1 ? SB1 : bi == 2 ? SB2 : SB3;
+        const float sj = bj == 0 ? SE0 : bj == 1 ? SE1 : SE2;
+        pf = si == sj ? pf : 0.f;
+        sm.seg[NB][s] = sg;
+    }
     sm.gcum[NB][s] = G;
     sm.gam[NB][s] = gam;
-    sm.gdl[NB][s] = __expf(Glast - G);
+    sm.gdl[NB][s] = gdl;
     sm.nbg[NB][s] = -beta * gam;
     sm.bs[NB][s] = beta;
-    sm.dst[NB][s] = __expf(G - Gs);
-    sm.den[NB][s] = __expf(Ge - G);
-    if (s < 16) {
-        const int bi = s >> 2, bj = s & 3;
-        const float gi = bi == 0 ? B0 : bi == 1 ? B1 : bi == 2 ? B2 : B3;
-        const float gj = bj == 0 ? E0 : bj == 1 ? E1 : bj == 2 ? E2 : Glast;
-        sm.pf[NB][s] = bi > bj ? __expf(gi - gj) : 0.f;
-    }
+    sm.dst[NB][s] = dst;
+    sm.den[NB][s] = den;
+    if (s < 16) sm.pf[NB][s] = pf;
+    if (s == 0) sm.resets[NB] = SEG;
+}
+template <int DK, int NB>
+__device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, int s, int len, const ChunkIn<DK>& r) {
+    const float graw = log_decay(r.g, p.gate_is_alpha);
+    const bool rst = s < len && is_reset(graw);
+    const float g = s < len && !rst ? graw : 0.f;
+    const float beta = s < len ? r.b : 0.f;
+    if (__builtin_amdgcn_ballot_w64(rst) == 0)
+        stage_gates_as<DK, NB, false>(sm, s, g, beta, rst);
+    else
+        stage_gates_as<DK, NB, true>(sm, s, g, beta, rst);
 }
 
 // Chunk inputs from registers into LDS buffer NB: K and Q as fp16, beta V
@@ -553,9 +636,10 @@ __device__ __forceinline__ void load_rows(const uint16_t* src, int blk, int n, i
 // (beta and decay applied) or P (decay applied) in fp16; the decay is the
 // product of three factors <= 1, exp(G_r - G_{16 BI}) exp(G_{16 BI} -
 // G_{16 BJ + 15}) exp(G_{16 BJ + 15} - G_s).  Diagonal blocks are masked to
-// s < r (A, kept in fp32 for the substitution) or s <= r (P).
+// s < r (A, kept in fp32 for the substitution) or s <= r (P).  The fp16
+// values pass through rng's range watch.
 template <int DK, int NB, bool ISQ, int BI, int BJ>
-__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l) {
+__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
     constexpr bool diag = BI == BJ;
     const int n = l & 15, g = l >> 4;
@@ -565,6 +649,7 @@ __device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f1
     const float Gr = sm.gcum[NB][r];
     const float fr = diag ? 0.f : sm.dst[NB][r] * sm.pf[NB][4 * BI + BJ];
     const f32x4 es = ld_f32x4(diag ? &sm.gcum[NB][s0] : &sm.den[NB][s0]);
+    const int resets = diag ? __builtin_amdgcn_readfirstlane(sm.resets[NB]) : 0;
     __builtin_amdgcn_sched_barrier(0);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -574,7 +659,9 @@ __device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f1
         const float f = fr * br;
 #pragma unroll
         for (int v = 0; v < 4; ++v) x[v] = acc[v] * f * es[v];
-        *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = pack_f16x4(x);
+        const uint2 h = pack_f16x4(x);
+        range_watch(rng, h);
+        *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = h;
     } else {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -582,10 +669,19 @@ __device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f1
             const bool keep = ISQ ? (s <= r) : (s < r);
             x[v] = keep ? acc[v] * br * __expf(Gr - es[v]) : 0.f;
         }
-        if constexpr (ISQ)
-            *reinterpret_cast<uint2*>(&sm.p[NB][toff(r, s0)]) = pack_f16x4(x);
-        else
+        if (resets) {  // only pairs in one segment (no reset in (s, r])
+            const float sr = sm.seg[NB][r];
+            const f32x4 ss = ld_f32x4(&sm.seg[NB][s0]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) x[v] = ss[v] == sr ? x[v] : 0.f;
+        }
+        if constexpr (ISQ) {
+            const uint2 h = pack_f16x4(x);
+            range_watch(rng, h);
+            *reinterpret_cast<uint2*>(&sm.p[NB][toff(r, s0)]) = h;
+        } else {
             *reinterpret_cast<float4*>(&sm.ad[(16 * BI + n) * kLDD + 4 * g]) = make_float4(x[0], x[1], x[2], x[3]);
+        }
     }
 }
 
@@ -700,10 +796,11 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim) 
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
-    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l);
-    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l);
-    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l);
-    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l);
+    uint32_t unused = 0;  // diagonal blocks of A stay fp32
+    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l, unused);
+    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l, unused);
+    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l, unused);
+    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l, unused);
     lds_fence();
     t_diag<DK, B>(sm, l);
     signal(&sm.sync.tdiag);
@@ -718,7 +815,7 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim) 
 
 // Wave 3, chunk x: K K^T below the diagonal into A, then T_32, T_21, T_31.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim) {
+__device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, uint32_t& rng) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     // K[B] staged; A (one buffer) was read by T's blocks of chunk x - 1
@@ -726,12 +823,12 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim) 
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
-    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l);
-    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l);
-    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l);
-    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l);
-    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l);
-    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l);
+    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l, rng);
+    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l, rng);
+    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l, rng);
+    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l, rng);
+    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l, rng);
+    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l, rng);
     signal(&sm.sync.aoff);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
@@ -744,7 +841,7 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim) 
 // Q K^T blocks of loader wave LW (0..3) for buffer NB:
 //   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)   LW 3: (3,1) (3,2) (3,3)
 template <int DK, int NB, int LW>
-__device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
+__device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
@@ -752,30 +849,30 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 0, n, g, y0);
         load_rows<DK>(sm.q[NB], 1, n, g, y1);
-        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l);
-        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l);
+        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l, rng);
+        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l, rng);
     } else if constexpr (LW == 1) {
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.q[NB], 1, n, g, y0);
         load_rows<DK>(sm.q[NB], 2, n, g, y1);
-        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l);
-        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l);
+        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l, rng);
+        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l, rng);
     } else if constexpr (LW == 2) {
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 2, n, g, y0);
         load_rows<DK>(sm.q[NB], 3, n, g, y1);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l);
-        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l);
-        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l);
+        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l, rng);
+        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l, rng);
+        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l, rng);
     } else {
         load_rows<DK>(sm.q[NB], 3, n, g, y0);
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l);
-        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l);
+        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l, rng);
+        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l, rng);
         load_rows<DK>(sm.k[NB], 3, n, g, x0);
-        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l);
+        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l, rng);
     }
 }
 
@@ -785,7 +882,7 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l) {
 template <int DK, int B, int LW>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, const LoadOffsets<DK>& lastc,
-                                            ChunkIn<DK>& in) {
+                                            ChunkIn<DK>& in, uint32_t& rng) {
     // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
     Sync& sy = sm.sync;
     wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
@@ -795,7 +892,7 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
     signal(&sm.sync.staged);
     load_chunk_any<DK>(p, u, x + 2, lo, lastc, in);
     wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
-    qk_blocks<DK, B, LW>(sm, lt & 63);
+    qk_blocks<DK, B, LW>(sm, lt & 63, rng);
     signal(&sm.sync.pdone);
 }
 
@@ -808,11 +905,13 @@ __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, 
     ChunkIn<DK> in0, in1;
     load_chunk_any<DK>(p, u, 0, lo, lastc, in0);
     load_chunk_any<DK>(p, u, 1, lo, lastc, in1);
+    uint32_t rng = 0;
     for (int x = 0; x < u.nch; x += 2) {
-        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, lastc, in0);
+        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, lastc, in0, rng);
         if (x + 1 >= u.nch) break;
-        prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, lastc, in1);
+        prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, lastc, in1, rng);
     }
+    note_range(rng);
 }
 
 // ------------------------------------------------------------ scan waves
@@ -1112,10 +1211,12 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
             if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l, p.spin_limit);
         }
     } else if (w == 3) {
+        uint32_t rng = 0;
         for (int x = 0; x < u.nch; x += 2) {
-            prep_wave3<DK, 0>(sm, x, l, p.spin_limit);
-            if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l, p.spin_limit);
+            prep_wave3<DK, 0>(sm, x, l, p.spin_limit, rng);
+            if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l, p.spin_limit, rng);
         }
+        note_range(rng);
     } else if (w == 4) {
         loader_loop<DK, 0>(p, sm, u, tid - 256);
     } else if (w == 5) {
@@ -1143,12 +1244,21 @@ size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a) {
     return a.cu_seqlens ? ((sizeof(int) * (size_t)a.batch + 255) & ~size_t(255)) : 0;
 }
 
-hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
-    hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_sync_timeouts), sizeof(unsigned int), 0,
-                                       hipMemcpyDeviceToHost);
+namespace {
+hipError_t read_counter(const void* symbol, unsigned int* count, bool reset) {
+    hipError_t e = hipMemcpyFromSymbol(count, symbol, sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
     if (e != hipSuccess || !reset) return e;
     const unsigned int zero = 0;
-    return hipMemcpyToSymbol(HIP_SYMBOL(g_sync_timeouts), &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+    return hipMemcpyToSymbol(symbol, &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+}
+}  // namespace
+
+hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
+    return read_counter(&g_sync_timeouts, count, reset);
+}
+
+hipError_t chunked_range_errors(unsigned int* count, bool reset) {
+    return read_counter(&g_range_errors, count, reset);
 }
 
 namespace {

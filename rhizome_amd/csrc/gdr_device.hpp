@@ -14,10 +14,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// Chunk length of the WY/UT prefill and the log-decay floor: a per-token
-// log-decay below kLogDecayFloor (alpha < 1.8e-35, including alpha = 0) is
-// raised to it, so every exponent stays finite; the state it carries over is
-// scaled by at most 1.8e-35.
+// Chunk length of the WY/UT prefill and its reset threshold: a token whose
+// log-decay is at or below kLogDecayFloor (alpha <= 1.8e-35, including
+// alpha = 0) starts a new segment inside its chunk -- everything before it is
+// forgotten exactly, as a reset does in the reference (delta.rs:137-142) --
+// and every other log-decay enters the chunk's prefix sums unchanged.
 constexpr int kChunk = 64;
 constexpr float kLogDecayFloor = -80.0f;
 
@@ -103,11 +104,14 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-// Gate value -> log-decay g (<= 0 expected), floored at kLogDecayFloor.
+// Gate value -> log-decay g (<= 0 expected; -inf for alpha = 0).
 __device__ __forceinline__ float log_decay(float gate, int gate_is_alpha) {
-    float g = gate_is_alpha ? logf(gate) : gate;
-    return fmaxf(g, kLogDecayFloor);  // also maps -inf (alpha = 0) and NaN-free logs
+    return gate_is_alpha ? logf(gate) : gate;
 }
+
+// Whether a log-decay resets the state (at or below kLogDecayFloor; a NaN
+// gate is no reset and carries into the outputs, as in the recurrence).
+__device__ __forceinline__ bool is_reset(float g) { return g <= kLogDecayFloor; }
 
 // Gate value -> alpha.
 __device__ __forceinline__ float decay_factor(float gate, int gate_is_alpha) {

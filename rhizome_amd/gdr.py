@@ -132,6 +132,17 @@ def sync_timeouts(reset: bool = True) -> int:
     return n.value
 
 
+def fp16_range_errors(reset: bool = True) -> int:
+    """Number of chunked-kernel steps on the current device since the last
+    reset whose fp16 operands formed from q and k were NaN, infinite or
+    beyond fp16's range (q, k or their inner products too large, or
+    non-finite q or k); 0 unless a chunked launch may have gone wrong.  Blocks until the device's
+    outstanding work is done."""
+    n = c_uint32(0)
+    _abi.check(_abi.lib().rhz_gdr_fp16_range_errors(byref(n), 1 if reset else 0))
+    return n.value
+
+
 def decode_args(q, k, v, gate, beta, gate_kind, state, o) -> _abi.DecodeArgs:
     B, H, dk = q.shape
     a = _abi.DecodeArgs()

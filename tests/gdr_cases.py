@@ -162,6 +162,7 @@ class Prefill:
         torch.cuda.synchronize()
         # no LDS wait of the chunked kernel gave up (the count is reset by the read)
         assert rhizome_amd.sync_timeouts() == 0, "a chunked-kernel LDS wait gave up"
+        assert rhizome_amd.fp16_range_errors() == 0, "a chunked-kernel fp16 operand out of range"
         return o.reshape(self.n_tok, self.heads, self.d_v), fin
 
     def oracle(self, seqs=None, heads=None):

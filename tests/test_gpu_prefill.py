@@ -93,6 +93,51 @@ def test_alpha_gate_with_resets(device, algo, dtype, tol):
 
 
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)
+@pytest.mark.parametrize("m", [37, 64, 70, 128])
+def test_reset_forgets_history(device, algo, dtype, tol, m):
+    """alpha = 0 at position m of every packed sequence (mid-chunk, at a chunk
+    start): the outputs from m on and the final states do not depend on the
+    initial state or on any input before m, bit for bit (a reset forgets S,
+    delta.rs:137-142).  Both histories keep the chunked path's power-of-two
+    state scale at 1, so its fp16 operands after the reset are the same
+    numbers."""
+    import rhizome_amd
+
+    lengths = [150, 200, 131]
+    w = Prefill(heads=2, d_k=64, d_v=64, lengths=lengths, dtype=dtype, device=device, state_std=0.02)
+    h = Prefill(heads=2, d_k=64, d_v=64, lengths=lengths, seed=1, dtype=dtype, device=device,
+                state_std=0.5)
+    starts = w.cu[:-1]
+    alpha64 = np.exp(w.g64)
+    alpha64[starts + m, :] = 0.0
+    alpha = torch.from_numpy(alpha64.astype(np.float32)).to(device)
+    w.alpha64 = alpha.double().cpu().numpy()
+    before = np.concatenate([np.arange(a, a + m) for a in starts])
+    after = np.setdiff1d(np.arange(w.n_tok), before)
+    bi = torch.from_numpy(before).to(device)
+    ai = torch.from_numpy(after).to(device)
+
+    def run(q, k, v, beta, a, init):
+        o, fin = rhizome_amd.prefill(q, k, v, None, beta, alpha=a, cu_seqlens=w.cu_dev,
+                                     initial_state=init, algo=algo)
+        torch.cuda.synchronize()
+        assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+        return o, fin
+
+    o1, f1 = run(w.q, w.k, w.v, w.beta, alpha, w.init)
+    _check(w, o1, f1, tol, tag=f"reset at {m} {algo} {dtype}")
+    other = []
+    for x, y in ((w.q, h.q), (w.k, h.k), (w.v, h.v), (w.beta, h.beta), (alpha, torch.exp(h.g))):
+        z = x.clone()
+        z[bi] = y[bi]
+        other.append(z)
+    o2, f2 = run(*other, h.init)
+    assert not torch.equal(o1[bi], o2[bi])
+    assert torch.equal(o1[ai], o2[ai]), "outputs after the reset depend on the history"
+    assert torch.equal(f1, f2), "final states depend on the history before the reset"
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
 @pytest.mark.parametrize("scale", [1e-4, 1e4])
 def test_value_magnitudes(device, algo, dtype, tol, scale):
     """v and S0 scaled by 1e-4 / 1e4: the op is linear in (v, S0) jointly; the
@@ -117,6 +162,43 @@ def test_query_scaled_by_sqrt_dk(device, algo, dtype, tol):
     w.q64 = w.q.double().cpu().numpy()
     o, fin = w.run(algo=algo)
     _check(w, o, fin, tol, tag=f"q * sqrt(d_k) {algo} {dtype}")
+
+
+def test_fp16_range_count(device):
+    """The chunked path's fp16 operands (q, k, and the q.k and k.k blocks)
+    against fp16's range, 65520.  q rows of norm 6e4 (so |q_r . k_s| <= 6e4)
+    stay inside: parity holds and nothing is counted.  One q element of 7e4,
+    or one infinite k element, is counted by rhz_gdr_fp16_range_errors; the
+    recurrent fp32 path takes the 7e4 input to the oracle's tolerance."""
+    import rhizome_amd
+
+    w = Prefill(batch=1, heads=2, seq_len=130, d_k=64, d_v=64, dtype=torch.bfloat16, device=device,
+                state_std=0.02)
+    w.q = (w.q.double() * 6e4).to(torch.bfloat16)
+    w.q64 = w.q.double().cpu().numpy()
+    assert float(np.abs(w.q64).max()) < 65520.0
+    rhizome_amd.fp16_range_errors(reset=True)
+    o, fin = w.run(algo="chunked")  # asserts a zero count
+    _check(w, o, fin, BF16_TOL, tag="q rows of norm 6e4, chunked")
+
+    def count(q, k):
+        rhizome_amd.prefill(w.shaped(q), w.shaped(k), w.shaped(w.v), w.shaped(w.g), w.shaped(w.beta),
+                            initial_state=w.init, algo="chunked")
+        torch.cuda.synchronize()
+        return rhizome_amd.fp16_range_errors(reset=True)
+
+    assert count(w.q, w.k) == 0
+    q_big = w.q.clone()
+    q_big[70, 1, 5] = 7e4
+    assert count(q_big, w.k) > 0, "a q element beyond fp16's range was not counted"
+    k_inf = w.k.clone()
+    k_inf[3, 0, 0] = float("inf")
+    assert count(w.q, k_inf) > 0, "an infinite k element was not counted"
+    assert rhizome_amd.fp16_range_errors() == 0
+    w.q = q_big
+    w.q64 = q_big.double().cpu().numpy()
+    o, fin = w.run(algo="recurrent")
+    _check(w, o, fin, BF16_TOL, tag="q element 7e4, recurrent")
 
 
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)
