@@ -363,6 +363,72 @@ def bench_aux(torch, steps, warmup):
     return out
 
 
+def bench_local(torch, steps, warmup):
+    """The Local block's mixer from its projections on config 1's shape:
+    rhz_gdr_local_prefill (prepare fused into the chunked prefill) against
+    rhz_gdr_prepare followed by rhz_gdr_prefill on the same inputs.  Both
+    are driven through the C ABI with prebuilt argument structs."""
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = PREFILL
+    B, T, H, dk, dv = c["batch"], c["seq_len"], c["heads"], c["d_k"], c["d_v"]
+    dev = torch.device("cuda:0")
+    bf16, f32 = torch.bfloat16, torch.float32
+    lead = (B, T)
+    q = rhizome_amd.philox_fill("normal", 0, 21, lead + (H, dk), bf16)
+    k = rhizome_amd.philox_fill("normal", 0, 22, lead + (H, dk), bf16)
+    v = rhizome_amd.philox_fill("normal", 0, 23, lead + (H, dv), bf16)
+    bl = rhizome_amd.philox_fill("normal", 0, 24, lead + (H,), f32)
+    al = rhizome_amd.philox_fill("normal", 0, 25, lead + (H,), f32)
+    a_log = rhizome_amd.philox_fill("normal", 0, 26, (H,), f32)
+    o = torch.empty(lead + (H, dv), dtype=bf16, device=dev)
+    fin = torch.empty((B, H, dv, dk), dtype=f32, device=dev)
+    qp, kp = torch.empty_like(q), torch.empty_like(k)
+    beta, g = torch.empty_like(bl), torch.empty_like(al)
+    stream = torch.cuda.current_stream()
+    lib, sp = _abi.lib(), ctypes.c_void_p(stream.cuda_stream or None)
+    scale = float(dk) ** 0.5
+
+    la = _abi.LocalArgs()
+    la.prefill = gdr.prefill_args(q, k, v, None, None, _abi.GATE_LOG_ALPHA, None, None, fin, o, "chunked")
+    la.q_scale = scale
+    la.beta_logit, la.alpha_logit, la.a_log = bl.data_ptr(), al.data_ptr(), a_log.data_ptr()
+    pa = _abi.PrepareArgs()
+    pa.tokens, pa.heads, pa.d_k, pa.dtype, pa.q_scale = B * T, H, dk, _abi.BF16, scale
+    pa.q_in, pa.k_in, pa.q_out, pa.k_out = q.data_ptr(), k.data_ptr(), qp.data_ptr(), kp.data_ptr()
+    pa.beta_logit, pa.alpha_logit, pa.a_log = bl.data_ptr(), al.data_ptr(), a_log.data_ptr()
+    pa.beta, pa.g = beta.data_ptr(), g.data_ptr()
+    fa = gdr.prefill_args(qp, kp, v, g, beta, _abi.GATE_LOG_ALPHA, None, None, fin, o, "chunked")
+    lap, pap, fap = ctypes.byref(la), ctypes.byref(pa), ctypes.byref(fa)
+
+    def fused():
+        _abi.check(lib.rhz_gdr_local_prefill(lap, sp))
+
+    def separate():
+        _abi.check(lib.rhz_gdr_prepare(pap, sp))
+        _abi.check(lib.rhz_gdr_prefill(fap, sp))
+
+    out = {}
+    for name, fn in (("fused", fused), ("separate", separate)):
+        info = settle(torch, fn, 1 / 2)
+        for _ in range(warmup):
+            fn()
+        out[name] = {"ms_per_step": time_region(torch, stream, fn, steps), **info}
+    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0:
+        raise RuntimeError("a chunked-kernel diagnostic counter is nonzero after the Local-block leg")
+    tokens = B * T
+    return {"metric": "Local-block mixer tokens/s (prepare + chunked prefill)",
+            "value": tokens / (out["fused"]["ms_per_step"] * 1e-3), "unit": "tokens/s",
+            "ms_per_step": out["fused"]["ms_per_step"],
+            "separate_ms_per_step": out["separate"]["ms_per_step"],
+            "separate_tokens_per_s": tokens / (out["separate"]["ms_per_step"] * 1e-3),
+            "config": {"workload": "rhz_gdr_local_prefill vs rhz_gdr_prepare + rhz_gdr_prefill",
+                       "batch": B, "heads": H, "seq_len": T, "d_k": dk, "d_v": dv,
+                       "inputs": "bf16 raw q/k projections and v, fp32 logits"},
+            "steps": steps, "warmup": warmup, "settle": out}
+
+
 def cpu_baseline(pre_host, dec_host):
     """f64 oracle on this host: reference three-pass step with per-call allocations."""
     import numpy as np
@@ -470,6 +536,7 @@ def main() -> int:
     dlms, dlbytes, dl_host = bench_decode(torch, min(args.warmup, 16), DECODE_LARGE)
     mms, mbytes, ms_info = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
     aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
+    local = bench_local(torch, min(args.steps, 50), min(args.warmup, 10))
     long_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), PREFILL_LONG,
                            "chunked GDR prefill, long context, slow decay", "prefill_long")
     vc = dict(PREFILL_VARLEN)
@@ -552,6 +619,7 @@ def main() -> int:
                                    "bytes_per_launch": mbytes, "launch_us": mms * 1e3},
                       "steps": min(args.steps, 50), "warmup": min(args.warmup, 20), **ms_info},
         "prologue_epilogue": aux,
+        "local_block": local,
         "device": device_info(torch),
     }
     if not args.no_cpu_baseline:

@@ -289,6 +289,30 @@ typedef struct rhz_gdr_prepare_args {
 
 rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* args, void* stream);
 
+/* rhz_gdr_prepare fused into the CHUNKED prefill: the Local block's mixer
+ * from its projections (SPEC.md:53-56).  `prefill` is as for
+ * rhz_gdr_prefill except that q and k are the raw projections, its gate and
+ * beta are not read (the logits below replace them) and its gate_kind is
+ * ignored.  As the kernel stages each 64-token chunk it applies prepare's
+ * maps -- q := l2norm(q) * q_scale, k := l2norm(k),
+ * beta := sigmoid(beta_logit), g := -softplus(a_log[h]) softplus(alpha_logit)
+ * (elementwise.rs:5-12, 36-42, 125-128) -- in fp32, without prepare's
+ * rounding of q and k to bf16, so the prepared q, k, beta and g never go
+ * through HBM.  The result is rhz_gdr_prepare followed by rhz_gdr_prefill up
+ * to that rounding.  bf16 and the CHUNKED algorithm only (AUTO resolves to
+ * it; anything else is RHZ_ERR_UNSUPPORTED); the workspace is the one
+ * rhz_gdr_prefill_workspace_size reports for `prefill`.  No counterpart in
+ * the reference, whose steps run one after the other on the CPU. */
+typedef struct rhz_gdr_local_args {
+    rhz_gdr_prefill_args prefill;
+    float q_scale;             /* SPEC.md:53: sqrt(d_k) */
+    const float* beta_logit;   /* [tokens, H] */
+    const float* alpha_logit;  /* [tokens, H] */
+    const float* a_log;        /* [H] */
+} rhz_gdr_local_args;
+
+rhz_status rhz_gdr_local_prefill(const rhz_gdr_local_args* args, void* stream);
+
 /* RMSNorm of every row of `dim` values with a learned scale, as the
  * per-head norm of the op's output (groupnorm_heads / rmsnorm,
  * norm.rs:8-13, 48-59): y = x / sqrt(mean(x^2) + eps) * scale.  y may alias

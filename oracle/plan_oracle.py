@@ -8,7 +8,7 @@ planner (rhizome_amd/host/rhizome_plan.cpp), never by the product.
   plan        crates/plan/src/arena.rs:83-144  (arena::plan)
   verify      crates/plan/src/arena.rs:49-61   (ArenaPlan::verify)
 
-Pins (tests/test_plan_oracle.py): the reference's own arena and graph unit
+Pins (tests/test_plan_exec.py:43-76): the reference's own arena and graph unit
 tests (arena.rs:146-227, graph.rs tests), a hand-computed plan of a
 three-node chain, and invariants that fix a wrong placement rule: every pair
 of tensors live together is disjoint, offsets are 256-aligned, a chain

@@ -46,6 +46,13 @@ class PrefillArgs(Structure):
     ]
 
 
+class LocalArgs(Structure):
+    _fields_ = [
+        ("prefill", PrefillArgs), ("q_scale", c_float),
+        ("beta_logit", c_void_p), ("alpha_logit", c_void_p), ("a_log", c_void_p),
+    ]
+
+
 class DecodeArgs(Structure):
     _fields_ = [
         ("batch", c_int32), ("heads", c_int32), ("d_k", c_int32), ("d_v", c_int32),
@@ -127,6 +134,8 @@ def lib():
         L.rhz_gdr_prefill.restype = c_int32
         L.rhz_gdr_prefill_noalloc.argtypes = [POINTER(PrefillArgs), c_void_p]
         L.rhz_gdr_prefill_noalloc.restype = c_int32
+        L.rhz_gdr_local_prefill.argtypes = [POINTER(LocalArgs), c_void_p]
+        L.rhz_gdr_local_prefill.restype = c_int32
         L.rhz_gdr_sync_timeouts.argtypes = [POINTER(c_uint32), c_int32]
         L.rhz_gdr_sync_timeouts.restype = c_int32
         L.rhz_gdr_fp16_range_errors.argtypes = [POINTER(c_uint32), c_int32]

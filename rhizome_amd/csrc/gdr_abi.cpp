@@ -164,7 +164,8 @@ rhz_status rhz_gdr_prefill_workspace_size(const rhz_gdr_prefill_args* args, size
 }
 
 namespace {
-rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit);
+rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit,
+                        const rhz::ChunkPrologue* pro = nullptr);
 }  // namespace
 
 rhz_status rhz_gdr_prefill(const rhz_gdr_prefill_args* args, void* stream) { return prefill_impl(args, stream, 0); }
@@ -189,6 +190,28 @@ rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* strea
     return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");
 }
 
+rhz_status rhz_gdr_local_prefill(const rhz_gdr_local_args* args, void* stream) {
+    if (!args) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    rhz_gdr_prefill_args a = args->prefill;
+    a.gate = args->alpha_logit;
+    a.beta = args->beta_logit;
+    a.gate_kind = RHZ_GATE_LOG_ALPHA;
+    int algo = 0;
+    rhz_status s = check_prefill(&a, false, &algo);
+    if (s != RHZ_OK) return s;
+    if (algo != RHZ_ALGO_CHUNKED)
+        return fail(RHZ_ERR_UNSUPPORTED, "the fused prologue runs on the CHUNKED path only (bf16, d_k 8..128)");
+    const int64_t tokens = a.cu_seqlens ? (int64_t)a.seq_len : (int64_t)a.batch * a.seq_len;
+    if (tokens > 0) {
+        if (!args->beta_logit) return fail(RHZ_ERR_INVALID_ARG, "beta_logit is NULL");
+        if (!args->alpha_logit) return fail(RHZ_ERR_INVALID_ARG, "alpha_logit is NULL");
+        if (!args->a_log) return fail(RHZ_ERR_INVALID_ARG, "a_log is NULL");
+    }
+    if (reinterpret_cast<uintptr_t>(args->a_log) % 4) return fail(RHZ_ERR_INVALID_ARG, "a_log must be 4-byte aligned");
+    const rhz::ChunkPrologue pro{args->a_log, args->q_scale};
+    return prefill_impl(&a, stream, 0, &pro);
+}
+
 rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset) {
     if (!count) return fail(RHZ_ERR_INVALID_ARG, "count is NULL");
     unsigned int n = 0;
@@ -210,7 +233,8 @@ rhz_status rhz_gdr_fp16_range_errors(uint32_t* count, int32_t reset) {
 }  // extern "C"
 
 namespace {
-rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit) {
+rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin_limit,
+                        const rhz::ChunkPrologue* pro) {
     int algo = 0;
     const rhz_status s = check_prefill(args, true, &algo);
     if (s != RHZ_OK) return s;
@@ -226,7 +250,7 @@ rhz_status prefill_impl(const rhz_gdr_prefill_args* args, void* stream, int spin
             if (reinterpret_cast<uintptr_t>(args->workspace) & 255u)
                 return fail(RHZ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
         }
-        return hip_status(rhz::launch_chunked(*args, st, spin_limit), "chunked prefill launch");
+        return hip_status(rhz::launch_chunked(*args, st, spin_limit, pro), "chunked prefill launch");
     }
     return hip_status(rhz::launch_recurrent(*args, st), "recurrent prefill launch");
 }

@@ -255,14 +255,6 @@ struct PrepParams {
     float q_scale;
 };
 
-__device__ __forceinline__ float sigmoid_f(float x) {  // elementwise.rs:5-12
-    if (x >= 0.f) return 1.f / (1.f + expf(-x));
-    const float e = expf(x);
-    return e / (1.f + e);
-}
-__device__ __forceinline__ float softplus_f(float x) {  // elementwise.rs:36-42
-    return x > 30.f ? x : log1pf(expf(x));
-}
 
 // A row of d elements as vectors of N: lane li of the row's G lanes holds
 // vectors li + G i, i < NV (zero beyond the row).

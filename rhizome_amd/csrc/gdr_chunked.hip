@@ -64,9 +64,42 @@
 #include "gdr_internal.hpp"
 
 namespace rhz {
+
+// Launch parameters of the chunked kernel.  The instances with the fused
+// prologue (rhz_gdr_local_prefill) are compiled apart, in
+// gdr_chunked_pre.hip, which includes this file: compiled with the plain
+// instances in one unit, the plain DK = 128 kernel's register allocation
+// changed (256 VGPRs and spills instead of 253 and none).
+struct ChunkParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* gate;
+    const float* beta;
+    const int* cu_seqlens;
+    const float* init;
+    float* fin;
+    uint16_t* o;
+    const int* order;  // [N] longest-first (packed batches), nullptr for dense
+    int batch, seq_len, heads, d_k, d_v, gate_is_alpha;
+    int n_tiles;     // ceil(d_v / 32)
+    int spin_limit;  // polls after which an LDS wait gives up (and is counted)
+    // Fused prologue (the kernel's PRE instances): q and k are the raw
+    // projections, gate holds alpha logits and beta holds beta logits.
+    const float* a_log;  // [H]
+    float q_scale;
+};
+
+// The fused-prologue instances' launch and device counters (compiled in
+// gdr_chunked_pre.hip).
+hipError_t chunked_go_prologue(const ChunkParams& cp, int dk, int blocks, hipStream_t st);
+// which: 0 = LDS waits that gave up, 1 = fp16 range errors.
+hipError_t chunked_prologue_counter(int which, unsigned int* count, bool reset);
+
 namespace {
 
-// Number of LDS waits that gave up since the last reset (per device).
+// Number of LDS waits that gave up since the last reset (per device and
+// compilation unit: the host adds the two units' counts).
 __device__ unsigned int g_sync_timeouts;
 // Number of (workgroup, wave) pairs since the last reset in which an fp16
 // entry of A or P (the MFMA operands formed from q and k) was NaN,
@@ -88,23 +121,9 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-struct ChunkParams {
-    const uint16_t* q;
-    const uint16_t* k;
-    const uint16_t* v;
-    const float* gate;
-    const float* beta;
-    const int* cu_seqlens;
-    const float* init;
-    float* fin;
-    uint16_t* o;
-    const int* order;  // [N] longest-first (packed batches), nullptr for dense
-    int batch, seq_len, heads, d_k, d_v, gate_is_alpha;
-    int n_tiles;     // ceil(d_v / 32)
-    int spin_limit;  // polls after which an LDS wait gives up (and is counted)
-};
 
 // LDS tile addressing.  Rows are unpadded and the 16-byte chunks of a row
 // are permuted by an XOR with a GF(2)-linear function of the row index.  The
@@ -205,6 +224,42 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {
 }
 __device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 u) {
     return make_uint4(bf16x2_to_f16x2(u.x), bf16x2_to_f16x2(u.y), bf16x2_to_f16x2(u.z), bf16x2_to_f16x2(u.w));
+}
+// The same with every value multiplied by f in fp32 before the rounding.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2_scaled(uint32_t u, float f) {
+    const f16x2 r = {(_Float16)(__uint_as_float(u << 16) * f), (_Float16)(__uint_as_float(u & 0xffff0000u) * f)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint4 bf16x8_to_f16x8_scaled(uint4 u, float f) {
+    return make_uint4(bf16x2_to_f16x2_scaled(u.x, f), bf16x2_to_f16x2_scaled(u.y, f),
+                      bf16x2_to_f16x2_scaled(u.z, f), bf16x2_to_f16x2_scaled(u.w, f));
+}
+// The prologue's maps in the hardware's approximate forms (v_exp_f32,
+// v_log_f32, v_rcp_f32: about 1 ulp each), for the loader waves:
+// sigmoid(x) = 1 / (1 + e^-x); softplus(x) = x past 15, else ln(1 + e^x)
+// (for x below about -17, 1 + e^x rounds to 1 and the result is 0, an
+// absolute error below 4e-8).
+__device__ __forceinline__ float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+__device__ __forceinline__ float fast_softplus(float x) { return x > 15.f ? x : __logf(1.f + __expf(x)); }
+// Sum of the squares of eight bf16 (products exact in fp32, bf16 dot2).
+__device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
+    float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.x), __builtin_bit_cast(bf16x2, u.x), 0.f,
+                                              false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.y), __builtin_bit_cast(bf16x2, u.y), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.z), __builtin_bit_cast(bf16x2, u.z), a, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.w), __builtin_bit_cast(bf16x2, u.w), a, false);
+}
+// Sum over aligned groups of G (4, 8 or 16) lanes by DPP within rows of 16:
+// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror.  The
+// pairings are symmetric, so every lane of a group gets the same bits.
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float x) {
+    static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
+    x += dpp_mov<0xB1>(x);
+    x += dpp_mov<0x4E>(x);
+    if constexpr (G >= 8) x += dpp_mov<0x141>(x);
+    if constexpr (G >= 16) x += dpp_mov<0x140>(x);
+    return x;
 }
 
 // Index (token of a chunk, or key column) carried by MFMA row m of 16-row
@@ -424,6 +479,7 @@ struct Smem {
 // Per-workgroup constants shared by the roles.
 struct Unit {
     int h, seq, tb, te, nch, i0;
+    float spa;  // fused prologue: softplus(a_log[h])
 };
 
 // ------------------------------------------------------------ loader waves
@@ -442,7 +498,7 @@ struct ChunkIn {
 template <int DK>
 struct LoadOffsets {
     uint32_t kq[DK / 32], v, g, bv;
-    __device__ void set(const ChunkParams& p, int i0, int lt, int last) {
+    __device__ __forceinline__ void set(const ChunkParams& p, int i0, int lt, int last) {
         constexpr int PPR = DK / 8;
         const uint32_t H = p.heads, dk = p.d_k, dv = p.d_v;
 #pragma unroll
@@ -548,12 +604,15 @@ __device__ __forceinline__ void stage_gates_as(Smem<DK>& sm, int s, float g, flo
     if (s < 16) sm.pf[NB][s] = pf;
     if (s == 0) sm.resets[NB] = SEG;
 }
-template <int DK, int NB>
-__device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, int s, int len, const ChunkIn<DK>& r) {
-    const float graw = log_decay(r.g, p.gate_is_alpha);
+// PRE: the gate and beta loaded are logits, mapped as the prologue does
+// (g = -softplus(a_h) softplus(alpha_logit), beta = sigmoid(beta_logit)).
+template <int DK, int NB, bool PRE>
+__device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int s, int len,
+                                            const ChunkIn<DK>& r) {
+    const float graw = PRE ? -u.spa * fast_softplus(r.g) : log_decay(r.g, p.gate_is_alpha);
     const bool rst = s < len && is_reset(graw);
     const float g = s < len && !rst ? graw : 0.f;
-    const float beta = s < len ? r.b : 0.f;
+    const float beta = s < len ? (PRE ? fast_sigmoid(r.b) : r.b) : 0.f;
     if (__builtin_amdgcn_ballot_w64(rst) == 0)
         stage_gates_as<DK, NB, false>(sm, s, g, beta, rst);
     else
@@ -563,10 +622,42 @@ __device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, 
 // Chunk inputs from registers into LDS buffer NB: K and Q as fp16, beta V
 // transposed, and (GATES: the gate wave) the gates.  Out-of-range rows and columns are
 // written as zeros.
-template <int DK, int NB, bool GATES>
-__device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, int len, int i0, int lt,
-                                            const ChunkIn<DK>& r) {
+//
+// PRE (the fused prologue): every K row is L2-normalised and every Q row
+// L2-normalised and multiplied by q_scale as it is staged
+// (elementwise.rs:125-128, x / max(||x||, 1e-12) * scale, in fp32 before the
+// rounding to fp16, the reciprocal norm by v_rsq_f32), and beta comes from
+// its logit.  A row's PPR 16-byte pieces lie on PPR consecutive lanes of one
+// wave, so its squared norm is a sum over those lanes.
+template <int DK, int NB, bool GATES, bool PRE>
+__device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, const Unit& un, int len, int i0,
+                                            int lt, const ChunkIn<DK>& r) {
     constexpr int PPR = DK / 8;
+    if constexpr (PRE) {
+        const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < DK / 32; ++u) {
+            const int it = lt + 256 * u, row = it / PPR, c8 = (it % PPR) * 8;
+            const bool ok = row < len && c8 < p.d_k;
+            const uint4 kk = ok ? r.k[u] : z, qq = ok ? r.q[u] : z;
+            // 1 / max(||x||, 1e-12) as rsq(max(||x||^2, 1e-24))
+            const float fk = __builtin_amdgcn_rsqf(fmaxf(lane_group_sum<PPR>(sumsq_bf16x8(kk)), 1e-24f));
+            const float fq = p.q_scale * __builtin_amdgcn_rsqf(fmaxf(lane_group_sum<PPR>(sumsq_bf16x8(qq)), 1e-24f));
+            *reinterpret_cast<uint4*>(&sm.k[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8_scaled(kk, fk);
+            *reinterpret_cast<uint4*>(&sm.q[NB][KQ<DK>::off(row, c8)]) = bf16x8_to_f16x8_scaled(qq, fq);
+        }
+        const int row = lt >> 2, c8 = (lt & 3) * 8;
+        const bool ok = row < len && i0 + c8 < p.d_v;
+        const float bv = fast_sigmoid(r.bv);
+        const uint32_t wv[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sm.vb[NB][(c8 + 2 * e) * kLDV + row] = ok ? bv * __uint_as_float(wv[e] << 16) : 0.f;
+            sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = ok ? bv * __uint_as_float(wv[e] & 0xffff0000u) : 0.f;
+        }
+        if constexpr (GATES) stage_gates<DK, NB, true>(p, sm, un, lt & 63, len, r);
+        return;
+    }
     const bool full = len == kChunk && p.d_k == DK && i0 + kTV <= p.d_v;  // uniform
     if (full) {
 #pragma unroll
@@ -613,7 +704,7 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, 
             sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = ok ? r.bv * __uint_as_float(wv[e] & 0xffff0000u) : 0.f;
         }
     }
-    if constexpr (GATES) stage_gates<DK, NB>(p, sm, lt & 63, len, r);
+    if constexpr (GATES) stage_gates<DK, NB, false>(p, sm, un, lt & 63, len, r);
 }
 
 // ------------------------------------------------------------ K K^T, Q K^T
@@ -879,7 +970,7 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
 // Loader wave LW, chunk x (buffer B = x & 1): stage x from registers, load
 // x + 2 into the same registers, then Q K^T of x.  Each register set has
 // two chunk periods to arrive.
-template <int DK, int B, int LW>
+template <int DK, int B, int LW, bool PRE>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, const LoadOffsets<DK>& lastc,
                                             ChunkIn<DK>& in, uint32_t& rng) {
@@ -888,7 +979,7 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
     wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
                 {x - 1, x - 1, 4 * (x - 1), x - 1, x - 1});
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
-    stage_chunk<DK, B, LW == kGateWave>(p, sm, len, u.i0, lt, in);
+    stage_chunk<DK, B, LW == kGateWave, PRE>(p, sm, u, len, u.i0, lt, in);
     signal(&sm.sync.staged);
     load_chunk_any<DK>(p, u, x + 2, lo, lastc, in);
     wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
@@ -896,7 +987,7 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
     signal(&sm.sync.pdone);
 }
 
-template <int DK, int LW>
+template <int DK, int LW, bool PRE>
 __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int lt) {
     if (u.nch <= 0) return;
     LoadOffsets<DK> lo, lastc;
@@ -907,9 +998,9 @@ __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, 
     load_chunk_any<DK>(p, u, 1, lo, lastc, in1);
     uint32_t rng = 0;
     for (int x = 0; x < u.nch; x += 2) {
-        prep_loader<DK, 0, LW>(p, sm, u, x, lt, lo, lastc, in0, rng);
+        prep_loader<DK, 0, LW, PRE>(p, sm, u, x, lt, lo, lastc, in0, rng);
         if (x + 1 >= u.nch) break;
-        prep_loader<DK, 1, LW>(p, sm, u, x + 1, lt, lo, lastc, in1, rng);
+        prep_loader<DK, 1, LW, PRE>(p, sm, u, x + 1, lt, lo, lastc, in1, rng);
     }
     note_range(rng);
 }
@@ -1139,7 +1230,8 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
 }
 
 // ------------------------------------------------------------ fused kernel
-template <int DK>
+// PRE: the fused prologue (raw q, k projections and gate / beta logits).
+template <int DK, bool PRE>
 __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     constexpr int NK = DK / 32;
     __shared__ __align__(16) Smem<DK> sm;
@@ -1156,6 +1248,7 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     seq_bounds(p.cu_seqlens, u.seq, p.seq_len, u.tb, u.te);
     u.nch = (u.te - u.tb + kChunk - 1) / kChunk;
     u.i0 = tile * kTV;
+    u.spa = PRE && u.nch > 0 ? softplus_f(p.a_log[u.h]) : 0.f;
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int dk = p.d_k, dv = p.d_v;
@@ -1218,24 +1311,50 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         }
         note_range(rng);
     } else if (w == 4) {
-        loader_loop<DK, 0>(p, sm, u, tid - 256);
+        loader_loop<DK, 0, PRE>(p, sm, u, tid - 256);
     } else if (w == 5) {
-        loader_loop<DK, 1>(p, sm, u, tid - 256);
+        loader_loop<DK, 1, PRE>(p, sm, u, tid - 256);
     } else if (w == 6) {
-        loader_loop<DK, 2>(p, sm, u, tid - 256);
+        loader_loop<DK, 2, PRE>(p, sm, u, tid - 256);
     } else {
-        loader_loop<DK, 3>(p, sm, u, tid - 256);
+        loader_loop<DK, 3, PRE>(p, sm, u, tid - 256);
     }
 }
 
+hipError_t read_counter(const void* symbol, unsigned int* count, bool reset) {
+    hipError_t e = hipMemcpyFromSymbol(count, symbol, sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess || !reset) return e;
+    const unsigned int zero = 0;
+    return hipMemcpyToSymbol(symbol, &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+}
+
+#ifndef RHZ_CHUNKED_PROLOGUE_TU
 template <int DK>
 hipError_t chunked_go(const ChunkParams& cp, int blocks, hipStream_t st) {
-    if (blocks > 0) hipLaunchKernelGGL(gdr_chunk_kernel<DK>, dim3(blocks), dim3(512), 0, st, cp);
+    if (blocks <= 0) return hipGetLastError();
+    if (cp.a_log) return chunked_go_prologue(cp, DK, blocks, st);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gdr_chunk_kernel<DK, false>), dim3(blocks), dim3(512), 0, st, cp);
     return hipGetLastError();
 }
+#endif
 
 }  // namespace
 
+#ifdef RHZ_CHUNKED_PROLOGUE_TU
+hipError_t chunked_go_prologue(const ChunkParams& cp, int dk, int blocks, hipStream_t st) {
+    if (dk == 32)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gdr_chunk_kernel<32, true>), dim3(blocks), dim3(512), 0, st, cp);
+    else if (dk == 64)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gdr_chunk_kernel<64, true>), dim3(blocks), dim3(512), 0, st, cp);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gdr_chunk_kernel<128, true>), dim3(blocks), dim3(512), 0, st, cp);
+    return hipGetLastError();
+}
+
+hipError_t chunked_prologue_counter(int which, unsigned int* count, bool reset) {
+    return read_counter(which == 0 ? &g_sync_timeouts : &g_range_errors, count, reset);
+}
+#else
 bool chunked_supported(int d_k, int d_v) {
     return d_k >= 8 && d_k <= 128 && d_k % 8 == 0 && d_v >= 8 && d_v % 8 == 0;
 }
@@ -1244,21 +1363,21 @@ size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a) {
     return a.cu_seqlens ? ((sizeof(int) * (size_t)a.batch + 255) & ~size_t(255)) : 0;
 }
 
-namespace {
-hipError_t read_counter(const void* symbol, unsigned int* count, bool reset) {
-    hipError_t e = hipMemcpyFromSymbol(count, symbol, sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
-    if (e != hipSuccess || !reset) return e;
-    const unsigned int zero = 0;
-    return hipMemcpyToSymbol(symbol, &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
-}
-}  // namespace
-
+// Both counters are the sum of this unit's and the fused-prologue unit's.
 hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
-    return read_counter(&g_sync_timeouts, count, reset);
+    unsigned int a = 0, b = 0;
+    hipError_t e = read_counter(&g_sync_timeouts, &a, reset);
+    if (e == hipSuccess) e = chunked_prologue_counter(0, &b, reset);
+    *count = a + b;
+    return e;
 }
 
 hipError_t chunked_range_errors(unsigned int* count, bool reset) {
-    return read_counter(&g_range_errors, count, reset);
+    unsigned int a = 0, b = 0;
+    hipError_t e = read_counter(&g_range_errors, &a, reset);
+    if (e == hipSuccess) e = chunked_prologue_counter(1, &b, reset);
+    *count = a + b;
+    return e;
 }
 
 namespace {
@@ -1296,12 +1415,13 @@ hipError_t noalloc_scratch(int** out) {
 
 // The chunked launch with the packed-batch order in `order_buf` (room for
 // a.batch ints; unused for dense batches).
-hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf);
+hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf,
+                               const ChunkPrologue* pro = nullptr);
 
 }  // namespace
 
-hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit) {
-    return launch_chunked_with(a, st, spin_limit, static_cast<int*>(a.workspace));
+hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, const ChunkPrologue* pro) {
+    return launch_chunked_with(a, st, spin_limit, static_cast<int*>(a.workspace), pro);
 }
 
 hipError_t launch_chunked_noalloc(const rhz_gdr_prefill_args& a, hipStream_t st) {
@@ -1315,8 +1435,11 @@ hipError_t launch_chunked_noalloc(const rhz_gdr_prefill_args& a, hipStream_t st)
 }
 
 namespace {
-hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf) {
+hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf,
+                               const ChunkPrologue* pro) {
     ChunkParams cp;
+    cp.a_log = pro ? pro->a_log : nullptr;
+    cp.q_scale = pro ? pro->q_scale : 1.f;
     cp.q = static_cast<const uint16_t*>(a.q);
     cp.k = static_cast<const uint16_t*>(a.k);
     cp.v = static_cast<const uint16_t*>(a.v);
@@ -1348,5 +1471,6 @@ hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, in
     return chunked_go<128>(cp, blocks, st);
 }
 }  // namespace
+#endif  // RHZ_CHUNKED_PROLOGUE_TU
 
 }  // namespace rhz

@@ -113,6 +113,14 @@ __device__ __forceinline__ float log_decay(float gate, int gate_is_alpha) {
 // gate is no reset and carries into the outputs, as in the recurrence).
 __device__ __forceinline__ bool is_reset(float g) { return g <= kLogDecayFloor; }
 
+// The prologue's elementwise maps (elementwise.rs:5-12, 36-42).
+__device__ __forceinline__ float sigmoid_f(float x) {
+    if (x >= 0.f) return 1.f / (1.f + expf(-x));
+    const float e = expf(x);
+    return e / (1.f + e);
+}
+__device__ __forceinline__ float softplus_f(float x) { return x > 30.f ? x : log1pf(expf(x)); }
+
 // Gate value -> alpha.
 __device__ __forceinline__ float decay_factor(float gate, int gate_is_alpha) {
     return gate_is_alpha ? gate : expf(gate);

@@ -25,9 +25,17 @@ hipError_t launch_multistep(const rhz_gdr_multistep_args& a, hipStream_t stream)
 // d_k <= 128, d_v % 8 == 0 and 16-byte aligned tensors.
 bool chunked_supported(int d_k, int d_v);
 size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a);
+// The fused prologue of rhz_gdr_local_prefill: a.q and a.k are the raw
+// projections, a.gate holds alpha logits and a.beta beta logits.
+struct ChunkPrologue {
+    const float* a_log;  // [H]
+    float q_scale;
+};
 // spin_limit: polls after which an LDS wait gives up; <= 0 for the built-in
-// limit (tests pass a tiny one to force give-ups).
-hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream, int spin_limit = 0);
+// limit (tests pass a tiny one to force give-ups).  pro: the fused prologue,
+// or nullptr.
+hipError_t launch_chunked(const rhz_gdr_prefill_args& a, hipStream_t stream, int spin_limit = 0,
+                          const ChunkPrologue* pro = nullptr);
 // The chunked launch of rhz_gdr_prefill_noalloc: the packed-batch order
 // lives in a static device array of kNoAllocMaxSeqs ints (a.workspace is
 // not used); the caller has checked a.batch <= kNoAllocMaxSeqs for packed

@@ -123,6 +123,38 @@ def prefill(q, k, v, g=None, beta=None, *, alpha=None, cu_seqlens=None, initial_
     return o, fin
 
 
+def local_prefill(q, k, v, beta_logit, alpha_logit, a_log, *, q_scale=None, cu_seqlens=None,
+                  initial_state=None, output_final_state=True, workspace=None, out=None,
+                  final_state=None, stream=None):
+    """rhz_gdr_prepare fused into the chunked prefill (rhz_gdr_local_prefill).
+
+    q, k are the raw projections (bf16), beta_logit / alpha_logit the gate
+    logits [.., H] fp32 and a_log [H] fp32; q_scale defaults to sqrt(d_k).
+    Returns (o, final_state or None), as :func:`prefill` does on the
+    prepared inputs.
+    """
+    n = _check_prefill_shapes(q, k, v, alpha_logit, beta_logit, cu_seqlens, initial_state)
+    H = q.shape[-2]
+    if a_log.shape != (H,) or a_log.dtype != torch.float32:
+        raise ValueError(f"a_log must be fp32 ({H},)")
+    o = out if out is not None else torch.empty(v.shape, dtype=q.dtype, device=q.device)
+    fin = final_state
+    if fin is None and output_final_state:
+        fin = torch.empty((n, H, v.shape[-1], q.shape[-1]), dtype=torch.float32, device=q.device)
+    la = _abi.LocalArgs()
+    la.prefill = prefill_args(q, k, v, None, None, _abi.GATE_LOG_ALPHA, cu_seqlens, initial_state,
+                              fin, o, "chunked")
+    la.q_scale = float(q.shape[-1]) ** 0.5 if q_scale is None else float(q_scale)
+    la.beta_logit, la.alpha_logit, la.a_log = _ptr(beta_logit), _ptr(alpha_logit), _ptr(a_log)
+    need = workspace_bytes(la.prefill)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if workspace is not None:
+        la.prefill.workspace, la.prefill.workspace_bytes = _ptr(workspace), workspace.numel()
+    _abi.check(_abi.lib().rhz_gdr_local_prefill(byref(la), _stream(stream)))
+    return o, fin
+
+
 def sync_timeouts(reset: bool = True) -> int:
     """Number of the chunked kernel's LDS waits that gave up on the current
     device since the last reset (0 unless a launch may have gone wrong).

@@ -125,6 +125,48 @@ def test_prefill_validation(over, status, msg):
     assert msg in _abi.last_error()
 
 
+def _local(**over):
+    la = _abi.LocalArgs()
+    pre = {k: v for k, v in over.items() if k not in ("q_scale", "beta_logit", "alpha_logit", "a_log")}
+    la.prefill = _prefill(gate=None, beta=None, **pre)
+    la.q_scale = over.get("q_scale", 11.3)
+    la.beta_logit = over.get("beta_logit", A)
+    la.alpha_logit = over.get("alpha_logit", A)
+    la.a_log = over.get("a_log", A)
+    return la
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(batch=0), _abi.ERR_INVALID_ARG, "batch"),
+    (dict(dtype=_abi.F32), _abi.ERR_UNSUPPORTED, "CHUNKED path only"),
+    (dict(algo=_abi.ALGO_RECURRENT), _abi.ERR_UNSUPPORTED, "CHUNKED path only"),
+    (dict(d_k=100), _abi.ERR_UNSUPPORTED, "CHUNKED path only"),
+    (dict(dtype=_abi.F32, algo=_abi.ALGO_CHUNKED), _abi.ERR_UNSUPPORTED, "bf16"),
+    (dict(beta_logit=None), _abi.ERR_INVALID_ARG, "beta_logit is NULL"),
+    (dict(alpha_logit=None), _abi.ERR_INVALID_ARG, "alpha_logit is NULL"),
+    (dict(a_log=None), _abi.ERR_INVALID_ARG, "a_log is NULL"),
+    (dict(a_log=A + 2), _abi.ERR_INVALID_ARG, "a_log must be 4-byte aligned"),
+    (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
+    (dict(k=A + 8), _abi.ERR_INVALID_ARG, "16-byte aligned"),
+    (dict(beta_logit=A + 1), _abi.ERR_INVALID_ARG, "4-byte aligned"),
+    (dict(cu_seqlens=A), _abi.ERR_WORKSPACE, "workspace is NULL"),
+])
+def test_local_prefill_validation(over, status, msg):
+    """rhz_gdr_local_prefill checks its prefill part as rhz_gdr_prefill does,
+    with the logits in place of gate and beta, and takes only the CHUNKED path."""
+    st = _abi.lib().rhz_gdr_local_prefill(byref(_local(**over)), None)
+    assert st == status, _abi.last_error()
+    assert msg in _abi.last_error()
+    assert _abi.lib().rhz_gdr_local_prefill(None, None) == _abi.ERR_INVALID_ARG
+
+
+def test_local_prefill_nothing_to_do_is_ok():
+    # no tokens and no final state: no pointer is needed or touched
+    la = _local(seq_len=0, q=None, k=None, v=None, o=None, final_state=None, beta_logit=None,
+                alpha_logit=None, a_log=None)
+    assert _abi.lib().rhz_gdr_local_prefill(byref(la), None) == _abi.OK, _abi.last_error()
+
+
 def test_prefill_workspace_alignment():
     st, need = _ws(_prefill(cu_seqlens=A))
     args = _prefill(cu_seqlens=A, workspace=A + 16, workspace_bytes=need)
