@@ -107,6 +107,7 @@ PROFILES = {
     "conv1d": "conv1d_kernel_bf16_t16384_c6144.md",
     "prepare": "prepare_kernel_bf16_t16384_h16_d128.md",
     "rmsnorm": "rmsnorm_kernel_bf16_rows262144_d128.md",
+    "local": "gdr_chunk_kernel_128_pro_local_b4_h16_t4096_d128.md",
 }
 
 
@@ -244,7 +245,7 @@ def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
             "config": {"workload": workload, **cfg},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles(profile_key),
-                         "kernel": "gdr_chunk_kernel<128>", "algorithmic_bytes": nbytes,
+                         "kernel": "gdr_chunk_kernel<128, false>", "algorithmic_bytes": nbytes,
                          "launch_us": ms * 1e3,
                          "mfma": {"achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                                   "frac": tflops / PEAK_MFMA_TFLOPS, "flops_per_launch": flops}}}
@@ -418,9 +419,17 @@ def bench_local(torch, steps, warmup):
     if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0:
         raise RuntimeError("a chunked-kernel diagnostic counter is nonzero after the Local-block leg")
     tokens = B * T
+    # raw q, k, v read and o written once (bf16), two fp32 logits per
+    # (token, head), fp32 final states, a_log
+    nbytes = float(tokens * H * (3 * dk * 2 + dv * 2 + 2 * 4) + B * H * dv * dk * 4 + H * 4)
+    gbs = nbytes / (out["fused"]["ms_per_step"] * 1e-3) / 1e9
     return {"metric": "Local-block mixer tokens/s (prepare + chunked prefill)",
             "value": tokens / (out["fused"]["ms_per_step"] * 1e-3), "unit": "tokens/s",
             "ms_per_step": out["fused"]["ms_per_step"],
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles("local"),
+                         "kernel": "gdr_chunk_kernel<128, true>", "bytes_per_launch": nbytes,
+                         "launch_us": out["fused"]["ms_per_step"] * 1e3},
             "separate_ms_per_step": out["separate"]["ms_per_step"],
             "separate_tokens_per_s": tokens / (out["separate"]["ms_per_step"] * 1e-3),
             "config": {"workload": "rhz_gdr_local_prefill vs rhz_gdr_prepare + rhz_gdr_prefill",
@@ -577,7 +586,7 @@ def main() -> int:
         # is reported beside it.
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": gbs / PEAK_HBM_GBS, "traffic": traffic,
-                     "kernel": "gdr_chunk_kernel<128>", "algorithmic_bytes": algo_bytes,
+                     "kernel": "gdr_chunk_kernel<128, false>", "algorithmic_bytes": algo_bytes,
                      "launch_us": ms * 1e3,
                      "mfma": {"achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                               "frac": achieved / PEAK_MFMA_TFLOPS, "flops_per_launch": flops}},

@@ -230,7 +230,7 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2_scaled(uint32_t u, float f) 
     const f16x2 r = {(_Float16)(__uint_as_float(u << 16) * f), (_Float16)(__uint_as_float(u & 0xffff0000u) * f)};
     return __builtin_bit_cast(uint32_t, r);
 }
-__device__ __forceinline__ uint4 bf16x8_to_f16x8_scaled(uint4 u, float f) {
+[[maybe_unused]] __device__ __forceinline__ uint4 bf16x8_to_f16x8_scaled(uint4 u, float f) {
     return make_uint4(bf16x2_to_f16x2_scaled(u.x, f), bf16x2_to_f16x2_scaled(u.y, f),
                       bf16x2_to_f16x2_scaled(u.z, f), bf16x2_to_f16x2_scaled(u.w, f));
 }
@@ -242,7 +242,7 @@ __device__ __forceinline__ uint4 bf16x8_to_f16x8_scaled(uint4 u, float f) {
 __device__ __forceinline__ float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float fast_softplus(float x) { return x > 15.f ? x : __logf(1.f + __expf(x)); }
 // Sum of the squares of eight bf16 (products exact in fp32, bf16 dot2).
-__device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
+[[maybe_unused]] __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
     float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.x), __builtin_bit_cast(bf16x2, u.x), 0.f,
                                               false);
     a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.y), __builtin_bit_cast(bf16x2, u.y), a, false);
@@ -328,6 +328,7 @@ __device__ __forceinline__ int rescale_shift(float m, int lo, int hi, int target
 }
 
 // ------------------------------------------------------------ varlen setup
+#ifndef RHZ_CHUNKED_PROLOGUE_TU  // launched by the plain unit's host code only
 // Longest-first order of the packed sequences (ties by index), so the
 // longest chunk loops start first.  Identity above kMaxSortSeqs sequences.
 __global__ __launch_bounds__(1024) void gdr_varlen_order_kernel(const int* cu, int n, int seq_len, int* order) {
@@ -352,6 +353,7 @@ __global__ __launch_bounds__(1024) void gdr_varlen_order_kernel(const int* cu, i
         order[rank] = i;
     }
 }
+#endif
 
 // Workgroup -> (unit = seq-order index * H + h, tile).  Consecutive
 // workgroup ids go round-robin to the 8 XCDs, so the tiles of one unit are
