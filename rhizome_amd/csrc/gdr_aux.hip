@@ -43,18 +43,26 @@ struct Vec {
         }
     }
     static __device__ __forceinline__ void load(const T* p, float (&x)[N]) { unpack(load_raw(p), x); }
+    // NT: a non-temporal store (streaming output that this kernel does not
+    // read back).
+    template <bool NT = false>
     static __device__ __forceinline__ void store(T* p, const float (&x)[N]) {
         if constexpr (!VEC) {
             Elem<T>::store(p, 0, x[0]);
         } else if constexpr (sizeof(T) == 4) {
-            *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+            const f32x4 v = {x[0], x[1], x[2], x[3]};
+            if constexpr (NT)
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+            else
+                *reinterpret_cast<f32x4*>(p) = v;
         } else {
-            uint4 u;
-            u.x = pack_bf16x2(x[0], x[1]);
-            u.y = pack_bf16x2(x[2], x[3]);
-            u.z = pack_bf16x2(x[4], x[5]);
-            u.w = pack_bf16x2(x[6], x[7]);
-            *reinterpret_cast<uint4*>(p) = u;
+            typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 u = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]),
+                             pack_bf16x2(x[6], x[7])};
+            if constexpr (NT)
+                __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
+            else
+                *reinterpret_cast<u32x4*>(p) = u;
         }
     }
 };
@@ -67,6 +75,8 @@ __host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_c
 // three previous inputs from x (or the sequence's initial state before its
 // start), so spans are independent and the grid covers tokens x channels.
 constexpr int kConvSpan = 16;
+constexpr bool kConvNT = true;  // y by non-temporal stores
+constexpr bool kRowNT = true;   // prepare's and RMSNorm's outputs by non-temporal stores
 
 struct ConvParams {
     const void* x;
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
 #pragma unroll
             for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
                 yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
-            V::store(y + (t0 + i) * C + c, yt);
+            V::template store<kConvNT>(y + (t0 + i) * C + c, yt);
 #pragma unroll
             for (int e = 0; e < N; ++e) {
                 a[0][e] = a[1][e];
@@ -207,7 +217,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
 #pragma unroll
         for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
             yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
-        V::store(y + t * C + c, yt);
+        V::template store<kConvNT>(y + t * C + c, yt);
 #pragma unroll
         for (int e = 0; e < N; ++e) {
             a[0][e] = a[1][e];
@@ -302,7 +312,7 @@ struct RowSlice {
                 float o[N];
 #pragma unroll
                 for (int e = 0; e < N; ++e) o[e] = f(j + e, v[i][e]);
-                V::store(row + j, o);
+                V::template store<kRowNT>(row + j, o);
             }
         }
     }

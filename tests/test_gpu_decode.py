@@ -79,3 +79,36 @@ def test_deterministic(device):
     o2 = rhizome_amd.decode_step(q[0], k[0], v[0], g[0], b[0], state=s2)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(s, s2)
+
+
+def test_streamed_state_matches_plain_path(device):
+    """A state past the streaming threshold (B=1024 H=16 d=128, 1.07 GB) is
+    read by non-temporal loads with two rows per thread; the arithmetic per
+    row is the same, so the result equals the plain path's (the same batch
+    in four quarters of 268 MB each) bit for bit, and a sample of heads
+    matches the oracle."""
+    B, H, d = 1024, 16, 128
+    f32 = torch.float32
+    q = rhizome_amd.philox_fill("unit_rows", 3, 1, (B, H, d), f32)
+    k = rhizome_amd.philox_fill("unit_rows", 3, 2, (B, H, d), f32)
+    v = rhizome_amd.philox_fill("normal", 3, 3, (B, H, d), f32)
+    b = rhizome_amd.philox_fill("sigmoid", 3, 4, (B, H), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 3, 5, (B, H), f32)
+    s0 = rhizome_amd.philox_fill("normal", 3, 6, (B, H, d, d), f32, std=0.02)
+    s1 = s0.clone()
+    o1 = rhizome_amd.decode_step(q, k, v, g, b, state=s1)
+    s2 = s0.clone()
+    o2 = torch.empty_like(o1)
+    for i in range(4):
+        sl = slice(256 * i, 256 * (i + 1))
+        o2[sl] = rhizome_amd.decode_step(q[sl], k[sl], v[sl], g[sl], b[sl], state=s2[sl])
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    sample = slice(0, B, 97)
+    ref_s = s0[sample].double().cpu().numpy().copy()
+    ref_o = O.decode_batched(q[sample].double().cpu().numpy(), k[sample].double().cpu().numpy(),
+                             v[sample].double().cpu().numpy(), np.exp(g[sample].double().cpu().numpy()),
+                             b[sample].double().cpu().numpy(), ref_s)
+    check_close(o1[sample].cpu().numpy(), ref_o, F32_TOL, "streamed decode o")
+    check_close(s1[sample].cpu().numpy(), ref_s, F32_TOL, "streamed decode state")
+    del s0, s1, s2
