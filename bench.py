@@ -6,9 +6,18 @@ B=4, H=16, T=4096, d_k=d_v=128, bf16 q/k/v, fp32 gates/state, chunk 64 --
 one step = one rhz_gdr_prefill over the whole batch (all heads), inputs
 resident in HBM.  Alongside (`decode`): the decode state update on B=256,
 H=16, d=128, fp32 state, one rhz_gdr_decode_step launch per step over 64
-steps, as HBM GB/s; (`multistep`) rhz_gdr_multistep over 8 positions on
-the same shape, as HBM GB/s; and (`prologue_epilogue`) the conv1d, prepare and
-per-head RMSNorm ops on the prefill workload's tokens, as HBM GB/s.
+steps, as HBM GB/s, and (`decode_large_state`) the same step with a 1.07 GB
+state (B=1024), four times the last-level cache; (`multistep`)
+rhz_gdr_multistep over 8 positions on the same shape, as HBM GB/s;
+(`prologue_epilogue`) the conv1d, prepare and per-head RMSNorm ops on the
+prefill workload's tokens, as HBM GB/s; (`local_block`)
+rhz_gdr_local_prefill, the prefill with prepare fused in, from raw
+projections on the prefill shape, beside rhz_gdr_prepare + rhz_gdr_prefill;
+(`prefill_long_context`, `prefill_varlen`) the chunked prefill on B=1, H=32,
+T=32768, d_v=256 with slow decay, and on 64 packed sequences of 128..8192
+tokens with initial states.  Every leg first runs a settle phase of untimed
+launches (`--settle-ms`, recorded per leg), then its warmup, then the timed
+launches.
 
 Inputs are synthetic and seeded: the reference's Philox-4x32-10 streams
 (q=1, k=2, v=3, beta=4, g=5, state=6), generated on the device by
@@ -25,8 +34,8 @@ crates/ops/src/delta.rs) on this host in the same run.
 the timed regions: HBM byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) read
 on that copy give the scale from counter units to bytes.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-                    [--calibration-copy]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--settle-ms MS]
+                    [--no-cpu-baseline] [--calibration-copy]
 """
 from __future__ import annotations
 
