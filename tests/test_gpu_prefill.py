@@ -93,6 +93,28 @@ def test_alpha_gate_with_resets(device, algo, dtype, tol):
 
 
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)
+def test_many_resets_per_chunk(device, algo, dtype, tol):
+    """alpha = 0 at random positions (about one token in twelve, so most
+    chunks hold several resets, some adjacent), at a chunk's first and last
+    token and on two consecutive tokens: every segment boundary inside a
+    chunk, in the diagonal and the off-diagonal 16-token blocks."""
+    w = Prefill(heads=3, d_k=64, d_v=96, lengths=[300, 64, 129, 1], dtype=dtype, device=device,
+                state_std=0.05, seed=4)
+    rng = np.random.default_rng(12)
+    alpha64 = np.exp(w.g64)
+    alpha64[rng.random(alpha64.shape) < 1 / 12] = 0.0
+    alpha64[[63, 64, 100, 101, 300 + 63], :] = 0.0
+    alpha = torch.from_numpy(alpha64.astype(np.float32)).to(device)
+    w.alpha64 = alpha.double().cpu().numpy()
+    import rhizome_amd
+    o, fin = rhizome_amd.prefill(w.q, w.k, w.v, None, w.beta, alpha=alpha, cu_seqlens=w.cu_dev,
+                                 initial_state=w.init, algo=algo)
+    torch.cuda.synchronize()
+    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+    _check(w, o, fin, tol, tag=f"many resets {algo} {dtype}")
+
+
+@pytest.mark.parametrize("algo,dtype,tol", PATHS)
 @pytest.mark.parametrize("m", [37, 64, 70, 128])
 def test_reset_forgets_history(device, algo, dtype, tol, m):
     """alpha = 0 at position m of every packed sequence (mid-chunk, at a chunk
