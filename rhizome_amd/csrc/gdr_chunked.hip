@@ -84,9 +84,11 @@ struct ChunkParams {
     int batch, seq_len, heads, d_k, d_v, gate_is_alpha;
     int n_tiles;     // ceil(d_v / 32)
     int spin_limit;  // polls after which an LDS wait gives up (and is counted)
-    // Fused prologue (the kernel's PRE instances): q and k are the raw
-    // projections, gate holds alpha logits and beta holds beta logits.
-    const float* a_log;  // [H]
+    // Fused prologue (the kernel's PRE instances, launched when prologue is
+    // set): q and k are the raw projections, gate holds alpha logits and beta
+    // holds beta logits.
+    int prologue;
+    const float* a_log;  // [H]; read only by workgroups with tokens
     float q_scale;
 };
 
@@ -1334,7 +1336,7 @@ hipError_t read_counter(const void* symbol, unsigned int* count, bool reset) {
 template <int DK>
 hipError_t chunked_go(const ChunkParams& cp, int blocks, hipStream_t st) {
     if (blocks <= 0) return hipGetLastError();
-    if (cp.a_log) return chunked_go_prologue(cp, DK, blocks, st);
+    if (cp.prologue) return chunked_go_prologue(cp, DK, blocks, st);
     hipLaunchKernelGGL(HIP_KERNEL_NAME(gdr_chunk_kernel<DK, false>), dim3(blocks), dim3(512), 0, st, cp);
     return hipGetLastError();
 }
@@ -1440,6 +1442,7 @@ namespace {
 hipError_t launch_chunked_with(const rhz_gdr_prefill_args& a, hipStream_t st, int spin_limit, int* order_buf,
                                const ChunkPrologue* pro) {
     ChunkParams cp;
+    cp.prologue = pro != nullptr;
     cp.a_log = pro ? pro->a_log : nullptr;
     cp.q_scale = pro ? pro->q_scale : 1.f;
     cp.q = static_cast<const uint16_t*>(a.q);

@@ -237,3 +237,27 @@ def test_local_prefill_is_deterministic_and_rejects_fp32(device):
     assert torch.equal(o1, o2) and torch.equal(f1, f2)
     with pytest.raises(rhizome_amd.gdr.GdrError, match="CHUNKED"):
         rhizome_amd.local_prefill(q.float(), k.float(), v.float(), bl, al, a)
+
+
+def test_local_prefill_empty_sequences_copy_the_state(device):
+    """No tokens, final states requested: the final state is the initial one,
+    and the logits and a_log (NULL here) are never read."""
+    from ctypes import byref
+
+    from rhizome_amd import _abi, gdr
+
+    H, dk, dv = 2, 64, 32
+    cu = torch.zeros(3, dtype=torch.int32, device=device)
+    init = torch.randn(2, H, dv, dk, device=device)
+    fin = torch.full_like(init, float("nan"))
+    q = torch.empty(0, H, dk, dtype=torch.bfloat16, device=device)
+    v = torch.empty(0, H, dv, dtype=torch.bfloat16, device=device)
+    o = torch.empty_like(v)
+    la = _abi.LocalArgs()
+    la.prefill = gdr.prefill_args(q, q, v, None, None, _abi.GATE_LOG_ALPHA, cu, init, fin, o, "chunked")
+    ws = torch.empty(256, dtype=torch.uint8, device=device)
+    la.prefill.workspace, la.prefill.workspace_bytes = ws.data_ptr(), ws.numel()
+    la.q_scale = 8.0
+    _abi.check(_abi.lib().rhz_gdr_local_prefill(byref(la), None))
+    torch.cuda.synchronize()
+    assert torch.equal(fin, init)
