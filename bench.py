@@ -233,6 +233,8 @@ def bench_prefill(torch, steps, warmup, c=None):
     ms = time_region(torch, stream, step, steps)
     if rhizome_amd.sync_timeouts() != 0:
         raise RuntimeError("a chunked-kernel LDS wait gave up during the benchmark")
+    if rhizome_amd.fp16_range_errors() != 0:
+        raise RuntimeError("a chunked-kernel fp16 operand was out of range during the benchmark")
     flops = prefill_flops(lengths, H, dk, dv)
     algo_bytes = prefill_bytes(n_tok, H, dk, dv, n_seq, init_state=init is not None)
     host = {"q": q, "k": k, "v": v, "g": g, "beta": beta, "tokens": n_tok, **info}
