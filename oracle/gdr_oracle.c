@@ -1,7 +1,7 @@
 /*
  * gdr_oracle.c -- CPU f64 oracle for the gated delta-rule (GDR) forward.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker, never the product:
+ * TEST INFRASTRUCTURE ONLY.  It is the reference that tests compare against, never the product:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * it.  The shipped library (rhizome_amd/librhizome_gdr.so) never links,
  * calls or falls back to anything here.

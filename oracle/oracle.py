@@ -1,8 +1,9 @@
 """ctypes front end of the CPU f64 oracle (oracle/gdr_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()``
-and the ``cpu_baseline`` leg of ``bench.py`` -- as the checker, never as the
-measured or shipped path.  The product library never calls into it.
+and the ``cpu_baseline`` leg of ``bench.py`` -- as the reference that
+results are compared against, never as the measured or shipped path.  The
+product library never calls into it.
 
 Every function here forwards to a C function that restates the f64
 reference (``crates/ops/src/delta.rs``, ``rng.rs``, ``elementwise.rs``);

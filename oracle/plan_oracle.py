@@ -1,6 +1,6 @@
 """Pure-Python restatement of the reference's plan-level IR and arena planner.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the C++
+TEST INFRASTRUCTURE ONLY: imported by tests/ as the reference for the C++
 planner (rhizome_amd/host/rhizome_plan.cpp), never by the product.
 
   bytes_for   crates/core/src/dtype.rs:32-55   (DType::bits, block_size, bytes_for)

@@ -1,4 +1,4 @@
-"""Pins the CPU f64 oracle (oracle/gdr_oracle.c) before it is trusted as the checker.
+"""Pins the CPU f64 oracle (oracle/gdr_oracle.c) before the GPU tests compare against it.
 
 * Philox-4x32-10 against Random123's published known-answer vectors
   (crates/ops/src/rng.rs:43-60 is Random123's philox4x32 with key
