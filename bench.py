@@ -648,7 +648,7 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": dlbytes / (dlms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": dlbytes / (dlms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          "traffic": traffic_from_profiles("decode_large"),
-                         "kernel": "gdr_decode_kernel<8,4,true,float>", "bytes_per_launch": dlbytes,
+                         "kernel": "gdr_decode_kernel<8,1,true,float,true>", "bytes_per_launch": dlbytes,
                          "launch_us": dlms * 1e3},
             "warmup": min(args.warmup, 16), "settle_launches": dl_host["settle_launches"]},
         "prefill_long_context": long_leg,

@@ -194,11 +194,14 @@ __global__ __launch_bounds__(256) void gdr_decode_kernel(StepParams p) {
         const float sk = group_sum<LPR>(dot16(s[pp], kr));
         const float sq = group_sum<LPR>(dot16(s[pp], qr));
         if (r < dv) {
+            // Contractions written out, so that every instance (P, NTL)
+            // rounds alike and the streamed and plain launches agree bit
+            // for bit.
             const float vi = Elem<T>::load(v, r);
-            const float c = beta * (vi - alpha * sk);
-            const float oi = alpha * sq + c * kq;
+            const float c = beta * fmaf(-alpha, sk, vi);
+            const float oi = fmaf(alpha, sq, c * kq);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
+            for (int e = 0; e < 16; ++e) s[pp][e] = fmaf(alpha, s[pp][e], c * kr[e]);
             store_slice<LPR, VEC, true>(S + (long)r * dk, li, dk, s[pp]);
             if (li == 0) Elem<T>::store(o, r, oi);
         }
@@ -273,10 +276,10 @@ __global__ __launch_bounds__(256) void gdr_multistep_kernel(MultiParams p) {
             const int r = rbase + pp * RPP;
             const float sk = group_sum<LPR>(dot16(s[pp], kr));
             const float sq = group_sum<LPR>(dot16(s[pp], qr));
-            const float c = be * (vr[pp] - alpha * sk);
-            const float oi = alpha * sq + c * kq;
+            const float c = be * fmaf(-alpha, sk, vr[pp]);
+            const float oi = fmaf(alpha, sq, c * kq);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[pp][e] = alpha * s[pp][e] + c * kr[e];
+            for (int e = 0; e < 16; ++e) s[pp][e] = fmaf(alpha, s[pp][e], c * kr[e]);
             if (r < dv) {
                 store_slice<LPR, VEC, true>(snap + (long)r * dk, li, dk, s[pp]);
                 if (li == 0) Elem<T>::store(op, th * dv + r, oi);
@@ -336,10 +339,10 @@ __global__ __launch_bounds__(64) void gdr_recurrent_kernel(SeqParams p) {
         const float kq = group_sum<LPR>(dot16(kr, qr));
         const float sk = group_sum<LPR>(dot16(s, kr));
         const float sq = group_sum<LPR>(dot16(s, qr));
-        const float c = be * (vi - alpha * sk);
-        const float oi = alpha * sq + c * kq;
+        const float c = be * fmaf(-alpha, sk, vi);
+        const float oi = fmaf(alpha, sq, c * kq);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = alpha * s[e] + c * kr[e];
+        for (int e = 0; e < 16; ++e) s[e] = fmaf(alpha, s[e], c * kr[e]);
         if (li == 0 && row_ok) Elem<T>::store(op, ((long)t * H + h) * dv + r, oi);
     }
     if (p.fin && row_ok) store_slice<LPR, VEC>(p.fin + ((long)unit * dv + r) * dk, li, dk, s);
@@ -357,11 +360,13 @@ hipError_t decode_go(const StepParams& sp, int units, int dv, hipStream_t st) {
     return hipGetLastError();
 }
 
-// A state of more than kStreamStateBytes is read by non-temporal loads, two
-// passes per thread: measured on B = 1024, H = 16, d = 128 (1.07 GB), 5.34
-// against 4.99 TB/s.  Below it the last-level cache (256 MB) keeps much of
-// the state between steps, and plain loads with four passes are faster
-// (B = 256, 268 MB: 6.24 against 5.49 TB/s).
+// A state of more than kStreamStateBytes is read by non-temporal loads, one
+// pass per thread: measured on B = 1024, H = 16, d = 128 (1.07 GB), 5.78-5.81
+// TB/s against 5.23-5.29 with two or four passes, 5.15 with plain stores
+// and 5.32 with plain loads.  Below it the last-level cache (256 MB) keeps
+// much of the state between steps, and plain loads with four passes are
+// faster (B = 256, 268 MB: 6.23 against 5.86 TB/s for one pass with
+// non-temporal loads and 5.65 with plain ones).
 constexpr size_t kStreamStateBytes = size_t(512) << 20;
 
 template <int LPR, bool VEC, typename T>
@@ -369,7 +374,7 @@ hipError_t decode_pick_p(const StepParams& sp, int units, int dv, hipStream_t st
     constexpr int RPP = 256 / LPR;
     const int passes = (dv + RPP - 1) / RPP;
     const bool stream = VEC && (size_t)units * dv * sp.d_k * sizeof(float) > kStreamStateBytes;
-    if (stream && passes >= 2) return decode_go<LPR, 2, VEC, T, true>(sp, units, dv, st);
+    if (stream) return decode_go<LPR, 1, VEC, T, true>(sp, units, dv, st);
     if (passes >= 4) return decode_go<LPR, 4, VEC, T>(sp, units, dv, st);
     if (passes == 3 || passes == 2) return decode_go<LPR, 2, VEC, T>(sp, units, dv, st);
     return decode_go<LPR, 1, VEC, T>(sp, units, dv, st);

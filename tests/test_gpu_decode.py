@@ -83,7 +83,7 @@ def test_deterministic(device):
 
 def test_streamed_state_matches_plain_path(device):
     """A state past the streaming threshold (B=1024 H=16 d=128, 1.07 GB) is
-    read by non-temporal loads with two rows per thread; the arithmetic per
+    read by non-temporal loads with one row per thread; the arithmetic per
     row is the same, so the result equals the plain path's (the same batch
     in four quarters of 268 MB each) bit for bit, and a sample of heads
     matches the oracle."""
