@@ -275,7 +275,7 @@ typedef struct rhz_gdr_prepare_args {
     int32_t heads;    /* H >= 1 */
     int32_t d_k;      /* 1..256 */
     int32_t dtype;    /* rhz_dtype of q and k, in and out */
-    float q_scale;    /* SPEC.md:53: sqrt(d_k) */
+    float q_scale;    /* SPEC.md:53: sqrt(d_k); must be finite */
     const void* q_in;          /* [tokens, H, d_k] */
     const void* k_in;          /* [tokens, H, d_k] */
     void* q_out;               /* [tokens, H, d_k] */
@@ -305,7 +305,7 @@ rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* args, void* stream);
  * the reference, whose steps run one after the other on the CPU. */
 typedef struct rhz_gdr_local_args {
     rhz_gdr_prefill_args prefill;
-    float q_scale;             /* SPEC.md:53: sqrt(d_k) */
+    float q_scale;             /* SPEC.md:53: sqrt(d_k); must be finite */
     const float* beta_logit;   /* [tokens, H] */
     const float* alpha_logit;  /* [tokens, H] */
     const float* a_log;        /* [H] */

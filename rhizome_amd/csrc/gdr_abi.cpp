@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -201,6 +202,7 @@ rhz_status rhz_gdr_local_prefill(const rhz_gdr_local_args* args, void* stream) {
     if (s != RHZ_OK) return s;
     if (algo != RHZ_ALGO_CHUNKED)
         return fail(RHZ_ERR_UNSUPPORTED, "the fused prologue runs on the CHUNKED path only (bf16, d_k 8..128)");
+    if (!std::isfinite(args->q_scale)) return fail(RHZ_ERR_INVALID_ARG, "q_scale must be finite");
     const int64_t tokens = a.cu_seqlens ? (int64_t)a.seq_len : (int64_t)a.batch * a.seq_len;
     if (tokens > 0) {
         if (!args->beta_logit) return fail(RHZ_ERR_INVALID_ARG, "beta_logit is NULL");
@@ -364,6 +366,7 @@ rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* a, void* stream) {
     if (a->d_k > 256) return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d exceeds the supported 256", a->d_k);
     if ((int64_t)a->tokens * a->heads * a->d_k > kMaxIndex)
         return fail(RHZ_ERR_INVALID_ARG, "tokens * heads * d_k exceeds 2^31 - 1");
+    if (!std::isfinite(a->q_scale)) return fail(RHZ_ERR_INVALID_ARG, "q_scale must be finite");
     if (a->tokens == 0) return ok();
     const void* ptrs[] = {a->q_in, a->k_in, a->q_out, a->k_out, a->beta_logit, a->alpha_logit, a->a_log,
                           a->beta, a->g};

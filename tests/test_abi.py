@@ -146,6 +146,8 @@ def _local(**over):
     (dict(alpha_logit=None), _abi.ERR_INVALID_ARG, "alpha_logit is NULL"),
     (dict(a_log=None), _abi.ERR_INVALID_ARG, "a_log is NULL"),
     (dict(a_log=A + 2), _abi.ERR_INVALID_ARG, "a_log must be 4-byte aligned"),
+    (dict(q_scale=float("nan")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
+    (dict(q_scale=float("inf")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
     (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
     (dict(k=A + 8), _abi.ERR_INVALID_ARG, "16-byte aligned"),
     (dict(beta_logit=A + 1), _abi.ERR_INVALID_ARG, "4-byte aligned"),
@@ -309,6 +311,7 @@ def _prep(**over):
     (dict(d_k=257), _abi.ERR_UNSUPPORTED, "256"), (dict(a_log=None), _abi.ERR_INVALID_ARG, "a_log is NULL"),
     (dict(g=A + 2), _abi.ERR_INVALID_ARG, "g is not aligned"),
     (dict(tokens=1 << 20, heads=64), _abi.ERR_INVALID_ARG, "2^31"),
+    (dict(q_scale=float("-inf")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
 ])
 def test_prepare_validation(over, status, msg):
     assert _abi.lib().rhz_gdr_prepare(byref(_prep(**over)), None) == status
