@@ -380,7 +380,7 @@ def bench_aux(torch, steps, warmup):
 
     jobs = {
         "conv1d": (conv, 2 * T * C * 2 + C * 20, "conv1d_kernel<bf16>", "B=1 T=16384, 6144 channels"),
-        "prepare": (prep, 4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<16,1,bf16,vec>",
+        "prepare": (prep, 4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<8,2,bf16,vec>",
                     "16384 tokens, H=16, d_k=128"),
         "rmsnorm": (norm, 2 * T * H * d * 2 + d * 4, "rmsnorm_kernel<16,1,bf16,vec>",
                     "16384 x 16 rows of 128"),
