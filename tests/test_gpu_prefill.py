@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from gdr_cases import (BF16_TOL, C0, C1, C2, C4, F32_TOL, Prefill, check_close, check_close_dev,
-                        nonexpansive_bound, varlen_lengths)
+                        nonexpansive_bound, to_device, varlen_lengths)
 
 pytestmark = pytest.mark.gpu
 
@@ -234,6 +234,30 @@ def test_query_scaled_by_sqrt_dk(device, algo, dtype, tol):
     w.q64 = w.q.double().cpu().numpy()
     o, fin = w.run(algo=algo)
     _check(w, o, fin, tol, tag=f"q * sqrt(d_k) {algo} {dtype}")
+
+
+def test_tiny_qk_entries(device):
+    """q and k entries below fp16's normal range (|x| < 2^-14): the chunked
+    path's bf16 -> fp16 conversion keeps them as fp16 subnormals, exact to
+    2^-25 absolute (a bf16 value there can carry more significant bits than
+    the subnormal keeps), so a dot product of unit rows moves by less than
+    d_k 2^-25.  Half of every row's entries drawn at 1e-7..1e-5, the rest
+    rescaled so that each row keeps unit norm; the chunked path stays within
+    its tolerance of the oracle on the same bf16 values."""
+    w = Prefill(batch=1, heads=2, seq_len=200, d_k=64, d_v=64, dtype=torch.bfloat16, device=device,
+                state_std=0.02, seed=9)
+    rng = np.random.default_rng(3)
+    for name in ("q", "k"):
+        x = getattr(w, name + "64").copy()
+        tiny = rng.random(x.shape) < 0.5
+        x[tiny] = np.sign(x[tiny]) * 10.0 ** rng.uniform(-7, -5, size=int(tiny.sum()))
+        x /= np.linalg.norm(x, axis=-1, keepdims=True)
+        t, x64 = to_device(x, torch.bfloat16, device)
+        assert float(np.mean(np.abs(x64) < 2.0 ** -14)) > 0.4
+        setattr(w, name, t)
+        setattr(w, name + "64", x64)
+    o, fin = w.run(algo="chunked")
+    _check(w, o, fin, BF16_TOL, tag="tiny q, k entries, chunked")
 
 
 def test_fp16_range_count(device):
