@@ -15,7 +15,8 @@ rhz_gdr_local_prefill, the prefill with prepare fused in, from raw
 projections on the prefill shape, beside rhz_gdr_prepare + rhz_gdr_prefill;
 (`prefill_long_context`, `prefill_varlen`) the chunked prefill on B=1, H=32,
 T=32768, d_v=256 with slow decay, and on 64 packed sequences of 128..8192
-tokens with initial states.  Every leg first runs a settle phase of untimed
+tokens with initial states; (`prefill_fp32`) the fp32-input path (the
+token-sequential recurrent kernel) on the headline prefill shape.  Every leg first runs a settle phase of untimed
 launches (`--settle-ms`, recorded per leg), then its warmup, then the timed
 launches.
 
@@ -53,6 +54,7 @@ sys.path.insert(0, ROOT)
 METRIC = "GDR prefill tokens/s + decode state-update HBM GB/s on 1 MI355X"
 PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 vector (packed)
 
 PREFILL = dict(batch=4, heads=16, seq_len=4096, d_k=128, d_v=128, chunk=64)
 # long context, slow decay: g = -softplus(N(-2, 1))
@@ -117,6 +119,7 @@ PROFILES = {
     "prepare": "prepare_kernel_bf16_t16384_h16_d128.md",
     "rmsnorm": "rmsnorm_kernel_bf16_rows262144_d128.md",
     "local": "gdr_chunk_kernel_128_pro_local_b4_h16_t4096_d128.md",
+    "prefill_fp32": "gdr_recurrent_kernel_prefill_fp32_b4_h16_t4096_d128.md",
 }
 
 
@@ -260,6 +263,63 @@ def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
                          "launch_us": ms * 1e3,
                          "mfma": {"achieved": tflops, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                                   "frac": tflops / PEAK_MFMA_TFLOPS, "flops_per_launch": flops}}}
+
+
+def bench_prefill_fp32(torch, steps, warmup) -> dict:
+    """The fp32-input path on the headline prefill shape: rhz_gdr_prefill with
+    fp32 q/k/v/o and RHZ_ALGO_RECURRENT (gdr_recurrent_kernel, token by token,
+    one wave per 8 state rows of a head)."""
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = PREFILL
+    B, T, H, dk, dv = c["batch"], c["seq_len"], c["heads"], c["d_k"], c["d_v"]
+    dev = torch.device("cuda:0")
+    f32 = torch.float32
+    lead = (B, T)
+    q = rhizome_amd.philox_fill("unit_rows", 0, 1, lead + (H, dk), f32)
+    k = rhizome_amd.philox_fill("unit_rows", 0, 2, lead + (H, dk), f32)
+    v = rhizome_amd.philox_fill("normal", 0, 3, lead + (H, dv), f32)
+    beta = rhizome_amd.philox_fill("sigmoid", 0, 4, lead + (H,), f32)
+    g = rhizome_amd.philox_fill("neg_softplus", 0, 5, lead + (H,), f32)
+    o = torch.empty(lead + (H, dv), dtype=f32, device=dev)
+    fin = torch.empty((B, H, dv, dk), dtype=f32, device=dev)
+    args = gdr.prefill_args(q, k, v, g, beta, _abi.GATE_LOG_ALPHA, None, None, fin, o, "recurrent")
+    stream = torch.cuda.current_stream()
+    lib, argp, sp = _abi.lib(), ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream or None)
+
+    def step():
+        st = lib.rhz_gdr_prefill(argp, sp)
+        if st:
+            _abi.check(st)
+
+    info = settle(torch, step, 1 / 2)
+    for _ in range(warmup):
+        step()
+    ms = time_region(torch, stream, step, steps)
+    tokens = B * T
+    nbytes = prefill_bytes(tokens, H, dk, dv, B, e_in=4, e_out=4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # the recurrence's own arithmetic, per token-head: S k, S q and k q, the
+    # rank-1 update and o (about 8 d_k d_v multiply-adds' worth; fp32 VALU)
+    flops = float(tokens * H * 8 * dk * dv)
+    return {"metric": "GDR prefill tokens/s, fp32 inputs", "value": tokens / (ms * 1e-3), "unit": "tokens/s",
+            "ms_per_step": ms, "steps": steps, "warmup": warmup, **info,
+            "config": {"workload": "recurrent GDR prefill, fp32 q/k/v/o", "batch": B, "heads": H,
+                       "seq_len": T, "d_k": dk, "d_v": dv, "inputs": "fp32 q/k/v, fp32 log-decay and beta",
+                       "state": "fp32"},
+            # token-sequential: every wave walks the T positions of its head
+            # one after the other, so the launch is bound by the per-position
+            # latency of that chain, not by HBM
+            "latency": {"ns_per_position": ms * 1e6 / T, "positions_per_wave": T,
+                        "waves": B * H * ((dv + 7) // 8)},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles("prefill_fp32"),
+                         "kernel": "gdr_recurrent_kernel<8,true,float>", "algorithmic_bytes": nbytes,
+                         "launch_us": ms * 1e3,
+                         "fp32_valu": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": PEAK_FP32_TFLOPS,
+                                       "unit": "TFLOP/s",
+                                       "frac": flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS}}}
 
 
 def bench_decode(torch, warmup, c=None):
@@ -583,6 +643,7 @@ def main() -> int:
     mms, mbytes, ms_info = bench_multistep(torch, min(args.steps, 50), min(args.warmup, 20))
     aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
     local = bench_local(torch, min(args.steps, 50), min(args.warmup, 10))
+    fp32_leg = bench_prefill_fp32(torch, min(args.steps, 20), min(args.warmup, 5))
     long_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), PREFILL_LONG,
                            "chunked GDR prefill, long context, slow decay", "prefill_long")
     vc = dict(PREFILL_VARLEN)
@@ -666,6 +727,7 @@ def main() -> int:
                       "steps": min(args.steps, 50), "warmup": min(args.warmup, 20), **ms_info},
         "prologue_epilogue": aux,
         "local_block": local,
+        "prefill_fp32": fp32_leg,
         "device": device_info(torch),
     }
     if not args.no_cpu_baseline:

@@ -206,18 +206,21 @@ rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* strea
 /* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
  * reference, whose op is a CPU loop).  The kernel's waves synchronise through
  * LDS counters with bounded waits; a wait that gives up lets the kernel end
- * and is counted on the device.  Writes the current device's count to *count
- * and, when reset is nonzero, sets it to zero.  Blocking: it waits for the
- * device's outstanding work.  A nonzero count means that some chunked launch
- * since the last reset may have produced wrong results. */
+ * and is counted on the device.  Blocking: it first waits for all of the
+ * current device's outstanding work, on every stream (hipDeviceSynchronize),
+ * then writes the device's count to *count and, when reset is nonzero, sets
+ * it to zero in the same atomic exchange on the device, so that a count added
+ * by a kernel launched meanwhile from another thread is kept for the next
+ * read, never lost.  A nonzero count means that some chunked launch since the
+ * last reset may have produced wrong results. */
 rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset);
 
 /* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
  * reference, whose op computes in f32 throughout): the number of
- * (workgroup, chunk, wave) steps since the last reset whose fp16 MFMA
- * operands formed from q and k on chip -- the blocks of beta K K^T and
- * Q K^T with their decays -- held a NaN, an infinity or a value of
- * magnitude 65520 or more.  That happens for q or k elements or inner
+ * (workgroup, wave) pairs, counted once per launch, since the last reset
+ * whose fp16 MFMA operands formed from q and k on chip -- the blocks of
+ * beta K K^T and Q K^T with their decays -- held a NaN, an infinity or a
+ * value of magnitude 65520 or more in any chunk.  That happens for q or k elements or inner
  * products beyond fp16's range and for non-finite q or k; a nonzero count
  * means that some chunked launch since the last reset may have produced
  * wrong results.  Same calling convention as rhz_gdr_sync_timeouts. */

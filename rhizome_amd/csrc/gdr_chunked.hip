@@ -1325,11 +1325,29 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     }
 }
 
-hipError_t read_counter(const void* symbol, unsigned int* count, bool reset) {
-    hipError_t e = hipMemcpyFromSymbol(count, symbol, sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
-    if (e != hipSuccess || !reset) return e;
-    const unsigned int zero = 0;
-    return hipMemcpyToSymbol(symbol, &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+// The value a counter held when read_counter swapped it (one per device and
+// compilation unit).
+__device__ unsigned int g_counter_read;
+
+// Reads counter `which` (0: g_sync_timeouts, 1: g_range_errors) into
+// g_counter_read and, when reset is set, zeroes it in the same atomic
+// exchange, so that a count added by a kernel still running elsewhere on the
+// device lands either in this read or in the next one, never in neither.
+__global__ __launch_bounds__(64) void gdr_counter_swap_kernel(int which, int reset) {
+    if (threadIdx.x != 0) return;
+    unsigned int* c = which == 0 ? &g_sync_timeouts : &g_range_errors;
+    g_counter_read = reset ? atomicExch(c, 0u) : __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits for all of the current device's work (every stream, blocking or
+// not), then swaps the counter on the null stream and copies the value out.
+hipError_t read_counter(int which, unsigned int* count, bool reset) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gdr_counter_swap_kernel, dim3(1), dim3(64), 0, nullptr, which, reset ? 1 : 0);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return hipMemcpyFromSymbol(count, HIP_SYMBOL(g_counter_read), sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
 }
 
 #ifndef RHZ_CHUNKED_PROLOGUE_TU
@@ -1356,7 +1374,7 @@ hipError_t chunked_go_prologue(const ChunkParams& cp, int dk, int blocks, hipStr
 }
 
 hipError_t chunked_prologue_counter(int which, unsigned int* count, bool reset) {
-    return read_counter(which == 0 ? &g_sync_timeouts : &g_range_errors, count, reset);
+    return read_counter(which, count, reset);
 }
 #else
 bool chunked_supported(int d_k, int d_v) {
@@ -1370,7 +1388,7 @@ size_t chunked_workspace_bytes(const rhz_gdr_prefill_args& a) {
 // Both counters are the sum of this unit's and the fused-prologue unit's.
 hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
     unsigned int a = 0, b = 0;
-    hipError_t e = read_counter(&g_sync_timeouts, &a, reset);
+    hipError_t e = read_counter(0, &a, reset);
     if (e == hipSuccess) e = chunked_prologue_counter(0, &b, reset);
     *count = a + b;
     return e;
@@ -1378,7 +1396,7 @@ hipError_t chunked_sync_timeouts(unsigned int* count, bool reset) {
 
 hipError_t chunked_range_errors(unsigned int* count, bool reset) {
     unsigned int a = 0, b = 0;
-    hipError_t e = read_counter(&g_range_errors, &a, reset);
+    hipError_t e = read_counter(1, &a, reset);
     if (e == hipSuccess) e = chunked_prologue_counter(1, &b, reset);
     *count = a + b;
     return e;

@@ -158,18 +158,21 @@ def local_prefill(q, k, v, beta_logit, alpha_logit, a_log, *, q_scale=None, cu_s
 def sync_timeouts(reset: bool = True) -> int:
     """Number of the chunked kernel's LDS waits that gave up on the current
     device since the last reset (0 unless a launch may have gone wrong).
-    Blocks until the device's outstanding work is done."""
+    Waits for all of the device's outstanding work on every stream first;
+    the read and the reset are one atomic exchange on the device."""
     n = c_uint32(0)
     _abi.check(_abi.lib().rhz_gdr_sync_timeouts(byref(n), 1 if reset else 0))
     return n.value
 
 
 def fp16_range_errors(reset: bool = True) -> int:
-    """Number of chunked-kernel steps on the current device since the last
-    reset whose fp16 operands formed from q and k were NaN, infinite or
-    beyond fp16's range (q, k or their inner products too large, or
-    non-finite q or k); 0 unless a chunked launch may have gone wrong.  Blocks until the device's
-    outstanding work is done."""
+    """Number of (workgroup, wave) pairs, counted once per chunked launch,
+    on the current device since the last reset whose fp16 operands formed
+    from q and k were NaN, infinite or beyond fp16's range in any chunk (q,
+    k or their inner products too large, or non-finite q or k); 0 unless a
+    chunked launch may have gone wrong.  Waits for all of the device's
+    outstanding work on every stream first; the read and the reset are one
+    atomic exchange on the device."""
     n = c_uint32(0)
     _abi.check(_abi.lib().rhz_gdr_fp16_range_errors(byref(n), 1 if reset else 0))
     return n.value

@@ -222,6 +222,38 @@ def test_local_prefill_matches_prepare_then_prefill(device, shape, with_state):
           f"prepare -> prefill normwise {sep:.3g}", flush=True)
 
 
+def test_local_prefill_config1_shape(device):
+    """rhz_gdr_local_prefill at the size it is benchmarked on (B=4, H=16,
+    T=4096, d=128, raw projections and logits as the bench draws them)
+    against the oracle's prepare -> prefill, every head."""
+    from gdr_cases import C1, check_close_dev
+
+    rng = _rng(57)
+    B, T, H, dk, dv = C1["batch"], C1["seq_len"], C1["heads"], C1["d_k"], C1["d_v"]
+    n_tok = B * T
+    q, q64 = to_device(rng.normal(size=(n_tok, H, dk)), torch.bfloat16, device)
+    k, k64 = to_device(rng.normal(size=(n_tok, H, dk)), torch.bfloat16, device)
+    v, v64 = to_device(rng.normal(size=(n_tok, H, dv)), torch.bfloat16, device)
+    bl, bl64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    al, al64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    a, a64 = to_device(rng.normal(size=H), torch.float32, device)
+    scale = float(dk) ** 0.5
+    lead = (B, T)
+    o, fin = rhizome_amd.local_prefill(q.view(lead + (H, dk)), k.view(lead + (H, dk)), v.view(lead + (H, dv)),
+                                       bl.view(lead + (H,)), al.view(lead + (H,)), a, q_scale=scale)
+    torch.cuda.synchronize()
+    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+    cu = np.arange(B + 1, dtype=np.int64) * T
+    rq, rk, rb, rg = O.prepare(q64, k64, bl64, al64, a64, scale)
+    ro, rf = O.prefill_batched(cu, rq, rk, v64, np.exp(rg), rb, None)
+    ro_d = torch.from_numpy(ro).to(device).transpose(0, 1).contiguous()
+    mo = check_close_dev(o.reshape(n_tok, H, dv).transpose(0, 1).contiguous(), ro_d, BF16_TOL,
+                         "fused c1 o", units=H)
+    del ro_d
+    mf = check_close_dev(fin, torch.from_numpy(rf).to(device), BF16_TOL, "fused c1 final state", units=B * H)
+    print(f"local prefill at B=4 H=16 T=4096 d=128: o {mo} final {mf}", flush=True)
+
+
 def test_local_prefill_is_deterministic_and_rejects_fp32(device):
     rng = _rng(41)
     H, dk, dv, T = 2, 64, 64, 200

@@ -135,3 +135,74 @@ def test_every_function_signature(both):
         assert [t for _, t in rparams] == [t for _, t in params], name
         assert rret == ret, name
 
+
+
+# ---- the safe drop-ins (src/lib.rs) behave as the reference and the tested
+# C++ layer do (rhizome_amd/host/rhizome_delta.cpp)
+
+def dropin_rust():
+    doc = open(DOC).read()
+    i = doc.index("### src/lib.rs: the drop-ins")
+    end = doc.index("## 3.", i)
+    blocks = re.findall(r"```rust\n(.*?)```", doc[i:end], flags=re.S)
+    assert len(blocks) == 2
+    return "\n".join(blocks)
+
+
+def rust_fn(text, name):
+    """The body of `pub fn name` up to its matching closing brace."""
+    i = text.index(f"pub fn {name}(")
+    j = text.index("{", text.index(")", i))
+    depth = 0
+    for k in range(j, len(text)):
+        depth += {"{": 1, "}": -1}.get(text[k], 0)
+        if depth == 0:
+            return text[j:k + 1]
+    raise AssertionError(f"unbalanced braces in {name}")
+
+
+def test_dropins_braces_balance():
+    text = re.sub(r"//[^\n]*", "", dropin_rust())
+    assert text.count("{") == text.count("}")
+    assert text.count("(") == text.count(")")
+
+
+def test_empty_sequence_returns_init():
+    # delta.rs:135,153: with T = 0 the loop never runs and init comes back
+    body = re.sub(r"//[^\n]*", "", rust_fn(dropin_rust(), "try_gated_delta_sequential"))
+    m = re.search(r"if t == 0 \{\s*return Ok\(\(Vec::new\(\), init\.clone\(\)\)\);\s*\}", body)
+    assert m, "T = 0 must return init unchanged"
+    # the early return comes before any device work
+    assert m.start() < body.index("DeviceBuf")
+    assert "vec![0.0; d * d]" not in body
+
+
+def test_lengths_checked_as_the_slicing_needs():
+    text = re.sub(r"//[^\n]*", "", dropin_rust())
+    # the reference never calls is_consistent (delta.rs:133-230)
+    assert "is_consistent" not in text
+    req = rust_fn(text, "require_inputs") if "pub fn require_inputs(" in text else None
+    if req is None:
+        i = text.index("fn require_inputs(")
+        req = text[i:text.index("\n}\n", i)]
+    for cond in ("inp.q.len() < t * d", "inp.k.len() < t * d", "inp.v.len() < t * d",
+                 "inp.beta.len() < t", "inp.segment.len() < t"):
+        assert cond in req, cond
+    # every sequence-level drop-in uses it
+    for fn in ("try_gated_delta_sequential", "gated_delta_multistep"):
+        assert "require_inputs(" in rust_fn(text, fn), fn
+
+
+def test_multistep_runs_in_windows():
+    # one rhz_gdr_multistep call takes at most RHZ_MULTISTEP_MAX positions;
+    # each window starts from the previous window's last snapshot
+    body = re.sub(r"//[^\n]*", "", rust_fn(dropin_rust(), "gated_delta_multistep"))
+    assert "sys::RHZ_MULTISTEP_MAX" in body
+    assert re.search(r"while t0 < n \{", body)
+    assert re.search(r"let m = window\.min\(n - t0\);", body)
+    assert re.search(r"steps: m as i32", body)
+    assert re.search(r"state: if t0 == 0 \{ f\(&s0, 0\) \} else \{ f\(&snaps, \(t0 - 1\) \* d \* d\) \}", body)
+    assert re.search(r"states: f\(&snaps, t0 \* d \* d\)", body)
+    assert "t0 += m;" in body
+    # no path hands n > RHZ_MULTISTEP_MAX to the ABI in one call
+    assert "steps: n as i32" not in body

@@ -4,8 +4,10 @@ Its only scratch (a packed batch's longest-first sequence order) is a static
 device array shared by every call on a GPU, so two calls in a row -- the
 second with fewer sequences -- must each match rhz_gdr_prefill (same kernels,
 caller-provided workspace) bit for bit.  A dense batch and the fp32
-recurrent path, which use no scratch, must match too.  The size limit is
-checked before any HIP call.
+recurrent path, which use no scratch, must match too.  A call captured in a
+HIP graph must match on every replay, with eager noalloc calls that
+overwrite the scratch in between; a batch of more than 4096 sequences takes
+the identity-order path.  The size limit is checked before any HIP call.
 """
 from ctypes import byref
 
@@ -28,6 +30,64 @@ def _noalloc(w, algo):
     torch.cuda.synchronize()
     assert rhizome_amd.sync_timeouts() == 0
     return o.reshape(w.n_tok, w.heads, w.d_v), fin
+
+
+def _noalloc_into(w, o, fin, stream):
+    """rhz_gdr_prefill_noalloc on workload w into preallocated o and fin."""
+    args = gdr.prefill_args(w.shaped(w.q), w.shaped(w.k), w.shaped(w.v), w.shaped(w.g), w.shaped(w.beta),
+                            _abi.GATE_LOG_ALPHA, w.cu_dev, w.init, fin, o, "chunked")
+    _abi.check(_abi.lib().rhz_gdr_prefill_noalloc(byref(args), stream))
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(device):
+    # Defined first in this file, so that (run alone or last) the captured
+    # call is normally the process's first noalloc call: the per-device
+    # scratch address is then looked up while the stream captures.
+    lengths = [int(x) for x in torch.randint(0, 300, (24,), generator=torch.Generator().manual_seed(7))]
+    lengths[3] = 0
+    w = Prefill(heads=2, d_k=128, d_v=64, lengths=lengths, seed=7, dtype=torch.bfloat16, device=device,
+                state_std=0.02)
+    o_ref, f_ref = w.run(algo="chunked")  # rhz_gdr_prefill, its own workspace
+    o_ref = o_ref.clone()
+    f_ref = f_ref.clone()
+    o = torch.empty_like(w.shaped(w.v))
+    fin = torch.empty((w.n_seqs, w.heads, w.d_v, w.d_k), dtype=torch.float32, device=device)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _noalloc_into(w, o, fin, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        o.fill_(float("nan"))
+        fin.fill_(float("nan"))
+        # eager work of the program between replays, including a noalloc
+        # call on a smaller batch that overwrites the shared scratch
+        small = Prefill(heads=1, d_k=32, d_v=32, lengths=[5, 70, 0, 33], seed=rep, dtype=torch.bfloat16,
+                        device=device)
+        o_s, f_s = _noalloc(small, "chunked")
+        o_s2, f_s2 = small.run(algo="chunked")
+        assert torch.equal(o_s, o_s2) and torch.equal(f_s, f_s2), f"eager noalloc, replay {rep}"
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert rhizome_amd.sync_timeouts() == 0
+        assert torch.equal(o.reshape(w.n_tok, w.heads, w.d_v), o_ref), f"o, replay {rep}"
+        assert torch.equal(fin, f_ref), f"final state, replay {rep}"
+        print(f"graph replay {rep}: noalloc == prefill, {w.n_seqs} sequences", flush=True)
+
+
+@pytest.mark.gpu
+def test_noalloc_more_sequences_than_the_sort(device):
+    # above 4096 packed sequences the order kernel writes the identity order,
+    # filling more of the shared scratch than the sorted path does
+    lengths = [int(x) for x in torch.randint(0, 6, (5000,), generator=torch.Generator().manual_seed(11))]
+    w = Prefill(heads=1, d_k=32, d_v=32, lengths=lengths, seed=11, dtype=torch.bfloat16, device=device,
+                state_std=0.02)
+    o1, f1 = _noalloc(w, "chunked")
+    o2, f2 = w.run(algo="chunked")
+    assert torch.equal(o1, o2) and torch.equal(f1, f2)
+    print(f"noalloc == prefill, {w.n_seqs} packed sequences, {w.n_tok} tokens", flush=True)
 
 
 @pytest.mark.gpu
