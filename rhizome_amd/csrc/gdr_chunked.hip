@@ -251,18 +251,6 @@ __device__ __forceinline__ float fast_softplus(float x) { return x > 15.f ? x : 
     a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.z), __builtin_bit_cast(bf16x2, u.z), a, false);
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.w), __builtin_bit_cast(bf16x2, u.w), a, false);
 }
-// Sum over aligned groups of G (4, 8 or 16) lanes by DPP within rows of 16:
-// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror.  The
-// pairings are symmetric, so every lane of a group gets the same bits.
-template <int G>
-__device__ __forceinline__ float lane_group_sum(float x) {
-    static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
-    x += dpp_mov<0xB1>(x);
-    x += dpp_mov<0x4E>(x);
-    if constexpr (G >= 8) x += dpp_mov<0x141>(x);
-    if constexpr (G >= 16) x += dpp_mov<0x140>(x);
-    return x;
-}
 
 // Index (token of a chunk, or key column) carried by MFMA row m of 16-row
 // block b: blocks 2c and 2c+1 together cover 32c .. 32c+31, and accumulator

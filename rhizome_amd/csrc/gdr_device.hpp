@@ -104,6 +104,19 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Sum over aligned groups of G (2, 4, 8 or 16) lanes by DPP within rows of
+// 16: quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror.
+// The pairings are symmetric, so every lane of a group gets the same bits.
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float x) {
+    static_assert(G == 2 || G == 4 || G == 8 || G == 16, "group of 2, 4, 8 or 16 lanes");
+    x += dpp_mov<0xB1>(x);
+    if constexpr (G >= 4) x += dpp_mov<0x4E>(x);
+    if constexpr (G >= 8) x += dpp_mov<0x141>(x);
+    if constexpr (G >= 16) x += dpp_mov<0x140>(x);
+    return x;
+}
+
 // Gate value -> log-decay g (<= 0 expected; -inf for alpha = 0).
 __device__ __forceinline__ float log_decay(float gate, int gate_is_alpha) {
     return gate_is_alpha ? logf(gate) : gate;
