@@ -16,7 +16,10 @@ projections on the prefill shape, beside rhz_gdr_prepare + rhz_gdr_prefill;
 (`prefill_long_context`, `prefill_varlen`) the chunked prefill on B=1, H=32,
 T=32768, d_v=256 with slow decay, and on 64 packed sequences of 128..8192
 tokens with initial states; (`prefill_fp32`) the fp32-input path (the
-token-sequential recurrent kernel) on the headline prefill shape.  Every leg first runs a settle phase of untimed
+token-sequential recurrent kernel) on the headline prefill shape;
+(`local_chain`) the whole Local-block mixer, from the q, k, v projections
+through conv1d, prepare, the prefill and the per-head RMSNorm, in three
+arrangements of the library's calls.  Every leg first runs a settle phase of untimed
 launches (`--settle-ms`, recorded per leg), then its warmup, then the timed
 launches.
 
@@ -120,6 +123,7 @@ PROFILES = {
     "rmsnorm": "rmsnorm_kernel_bf16_rows262144_d128.md",
     "local": "gdr_chunk_kernel_128_pro_local_b4_h16_t4096_d128.md",
     "prefill_fp32": "gdr_recurrent_kernel_prefill_fp32_b4_h16_t4096_d128.md",
+    "conv_prepare": "conv_prepare_kernel_bf16_t16384_h16_d128.md",
 }
 
 
@@ -438,12 +442,29 @@ def bench_aux(torch, steps, warmup):
     def norm():
         _abi.check(lib.rhz_rmsnorm_heads(rap, sp))
 
+    # conv1d and prepare in one pass over the same 6144 channels
+    vq, vk, vv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(q)
+    xa = _abi.ConvPrepareArgs()
+    xa.batch, xa.seq_len, xa.heads, xa.d_k, xa.d_v, xa.dtype = 1, T, H, d, d, _abi.BF16
+    xa.q_scale = float(d) ** 0.5
+    xa.x, xa.weight, xa.bias = x.data_ptr(), w.data_ptr(), cb.data_ptr()
+    xa.beta_logit, xa.alpha_logit, xa.a_log = lg.data_ptr(), lg.data_ptr(), a.data_ptr()
+    xa.q, xa.k, xa.v, xa.beta, xa.g = vq.data_ptr(), vk.data_ptr(), vv.data_ptr(), beta.data_ptr(), g.data_ptr()
+    xap = ctypes.byref(xa)
+
+    def convprep():
+        _abi.check(lib.rhz_gdr_conv_prepare(xap, sp))
+
     jobs = {
         "conv1d": (conv, 2 * T * C * 2 + C * 20, "conv1d_kernel<bf16>", "B=1 T=16384, 6144 channels"),
         "prepare": (prep, 4 * T * H * d * 2 + 4 * T * H * 4 + H * 4, "prepare_kernel<8,2,bf16,vec>",
                     "16384 tokens, H=16, d_k=128"),
         "rmsnorm": (norm, 2 * T * H * d * 2 + d * 4, "rmsnorm_kernel<16,1,bf16,vec>",
                     "16384 x 16 rows of 128"),
+        # x read and q, k, v written once (bf16), two fp32 logits read and
+        # beta, g written per (token, head), the conv weights and bias
+        "conv_prepare": (convprep, 2 * T * C * 2 + 4 * T * H * 4 + C * 20 + H * 4,
+                         "conv_prepare_kernel<bf16,16>", "B=1 T=16384, H=16, d_k=d_v=128 (6144 channels)"),
     }
     out = {}
     for name, (fn, nbytes, kernel, shape) in jobs.items():
@@ -533,6 +554,110 @@ def bench_local(torch, steps, warmup):
                        "batch": B, "heads": H, "seq_len": T, "d_k": dk, "d_v": dv,
                        "inputs": "bf16 raw q/k projections and v, fp32 logits"},
             "steps": steps, "warmup": warmup, "settle": out}
+
+
+def bench_local_chain(torch, steps, warmup):
+    """The whole Local-block mixer on config 1's shape (B=4, T=4096, H=16,
+    d=128, bf16), from the q, k, v projections and logits to the normed
+    output, in three arrangements of the library's calls:
+      separate:        conv1d (q, k, v) -> prepare -> prefill -> RMSNorm
+      fused_prologue:  conv1d (q, k, v) -> local_prefill -> RMSNorm
+      conv_prepare:    conv_prepare -> prefill -> RMSNorm
+    Each arrangement is one timed step of all its launches."""
+    import rhizome_amd
+    from rhizome_amd import _abi, gdr
+
+    c = PREFILL
+    B, T, H, d = c["batch"], c["seq_len"], c["heads"], c["d_k"]
+    N = B * T
+    C = 3 * H * d
+    dev = torch.device("cuda:0")
+    bf16, f32 = torch.bfloat16, torch.float32
+    x = rhizome_amd.philox_fill("normal", 0, 31, (N, C), bf16)
+    xq, xk, xv = (x[:, i * H * d:(i + 1) * H * d].contiguous() for i in range(3))
+    w = rhizome_amd.philox_fill("normal", 0, 32, (C, 4), f32, std=0.5)
+    wq, wk, wv = (w[i * H * d:(i + 1) * H * d].contiguous() for i in range(3))
+    bl = rhizome_amd.philox_fill("normal", 0, 33, (N, H), f32)
+    al = rhizome_amd.philox_fill("normal", 0, 34, (N, H), f32)
+    a_log = rhizome_amd.philox_fill("normal", 0, 35, (H,), f32)
+    sc = rhizome_amd.philox_fill("normal", 0, 36, (d,), f32)
+    yq, yk, yv = (torch.empty((N, H, d), dtype=bf16, device=dev) for _ in range(3))
+    q, k = torch.empty_like(yq), torch.empty_like(yk)
+    beta, g = torch.empty_like(bl), torch.empty_like(al)
+    o = torch.empty((N, H, d), dtype=bf16, device=dev)
+    y = torch.empty_like(o)
+    fin = torch.empty((B, H, d, d), dtype=f32, device=dev)
+    stream = torch.cuda.current_stream()
+    lib, sp = _abi.lib(), ctypes.c_void_p(stream.cuda_stream or None)
+    scale = float(d) ** 0.5
+
+    convs = []
+    for xi, wi, yi in ((xq, wq, yq), (xk, wk, yk), (xv, wv, yv)):
+        ca = _abi.Conv1dArgs()
+        ca.batch, ca.seq_len, ca.channels, ca.dtype = B, T, H * d, _abi.BF16
+        ca.x, ca.weight, ca.y = xi.data_ptr(), wi.data_ptr(), yi.data_ptr()
+        convs.append(ca)
+    pa = _abi.PrepareArgs()
+    pa.tokens, pa.heads, pa.d_k, pa.dtype, pa.q_scale = N, H, d, _abi.BF16, scale
+    pa.q_in, pa.k_in, pa.q_out, pa.k_out = yq.data_ptr(), yk.data_ptr(), q.data_ptr(), k.data_ptr()
+    pa.beta_logit, pa.alpha_logit, pa.a_log = bl.data_ptr(), al.data_ptr(), a_log.data_ptr()
+    pa.beta, pa.g = beta.data_ptr(), g.data_ptr()
+    sh = lambda t: t.view(B, T, *t.shape[1:])  # noqa: E731
+    fa = gdr.prefill_args(sh(q), sh(k), sh(yv), sh(g), sh(beta), _abi.GATE_LOG_ALPHA, None, None, fin, sh(o),
+                          "chunked")
+    la = _abi.LocalArgs()
+    la.prefill = gdr.prefill_args(sh(yq), sh(yk), sh(yv), None, None, _abi.GATE_LOG_ALPHA, None, None, fin,
+                                  sh(o), "chunked")
+    la.q_scale = scale
+    la.beta_logit, la.alpha_logit, la.a_log = bl.data_ptr(), al.data_ptr(), a_log.data_ptr()
+    xa = _abi.ConvPrepareArgs()
+    xa.batch, xa.seq_len, xa.heads, xa.d_k, xa.d_v, xa.dtype, xa.q_scale = B, T, H, d, d, _abi.BF16, scale
+    xa.x, xa.weight = x.data_ptr(), w.data_ptr()
+    xa.beta_logit, xa.alpha_logit, xa.a_log = bl.data_ptr(), al.data_ptr(), a_log.data_ptr()
+    xa.q, xa.k, xa.v, xa.beta, xa.g = q.data_ptr(), k.data_ptr(), yv.data_ptr(), beta.data_ptr(), g.data_ptr()
+    ra = _abi.RmsnormArgs()
+    ra.rows, ra.dim, ra.dtype, ra.eps = N * H, d, _abi.BF16, 1e-6
+    ra.x, ra.scale, ra.y = o.data_ptr(), sc.data_ptr(), y.data_ptr()
+    cps = [ctypes.byref(ca) for ca in convs]
+    pap, fap, lap, xap, rap = (ctypes.byref(t) for t in (pa, fa, la, xa, ra))
+
+    def conv3():
+        for cp in cps:
+            _abi.check(lib.rhz_causal_conv1d(cp, sp))
+
+    def separate():
+        conv3()
+        _abi.check(lib.rhz_gdr_prepare(pap, sp))
+        _abi.check(lib.rhz_gdr_prefill(fap, sp))
+        _abi.check(lib.rhz_rmsnorm_heads(rap, sp))
+
+    def fused_prologue():
+        conv3()
+        _abi.check(lib.rhz_gdr_local_prefill(lap, sp))
+        _abi.check(lib.rhz_rmsnorm_heads(rap, sp))
+
+    def conv_prepare():
+        _abi.check(lib.rhz_gdr_conv_prepare(xap, sp))
+        _abi.check(lib.rhz_gdr_prefill(fap, sp))
+        _abi.check(lib.rhz_rmsnorm_heads(rap, sp))
+
+    out = {}
+    for name, fn in (("separate", separate), ("fused_prologue", fused_prologue), ("conv_prepare", conv_prepare)):
+        info = settle(torch, fn, 1 / 3)
+        for _ in range(warmup):
+            fn()
+        ms = time_region(torch, stream, fn, steps)
+        out[name] = {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), **info}
+    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0:
+        raise RuntimeError("a chunked-kernel diagnostic counter is nonzero after the Local-block chain leg")
+    best = min(out, key=lambda n: out[n]["ms_per_step"])
+    return {"metric": "Local-block mixer tokens/s (conv1d + prepare + GDR prefill + per-head RMSNorm)",
+            "value": out[best]["tokens_per_s"], "unit": "tokens/s", "ms_per_step": out[best]["ms_per_step"],
+            "fastest": best, "arrangements": out,
+            "config": {"workload": "Local block from the q, k, v projections and logits to the normed output",
+                       "batch": B, "heads": H, "seq_len": T, "d_k": d, "d_v": d,
+                       "inputs": "bf16 projections, fp32 logits, fp32 conv weights"},
+            "steps": steps, "warmup": warmup}
 
 
 def cpu_baseline(pre_host, dec_host):
@@ -644,6 +769,7 @@ def main() -> int:
     aux = bench_aux(torch, min(args.steps, 50), min(args.warmup, 20))
     local = bench_local(torch, min(args.steps, 50), min(args.warmup, 10))
     fp32_leg = bench_prefill_fp32(torch, min(args.steps, 20), min(args.warmup, 5))
+    chain = bench_local_chain(torch, min(args.steps, 30), min(args.warmup, 5))
     long_leg = prefill_leg(torch, min(args.steps, 50), min(args.warmup, 10), PREFILL_LONG,
                            "chunked GDR prefill, long context, slow decay", "prefill_long")
     vc = dict(PREFILL_VARLEN)
@@ -728,6 +854,7 @@ def main() -> int:
         "prologue_epilogue": aux,
         "local_block": local,
         "prefill_fp32": fp32_leg,
+        "local_chain": chain,
         "device": device_info(torch),
     }
     if not args.no_cpu_baseline:

@@ -316,6 +316,49 @@ typedef struct rhz_gdr_local_args {
 
 rhz_status rhz_gdr_local_prefill(const rhz_gdr_local_args* args, void* stream);
 
+/* The Local block's prologue in one HBM pass (SPEC.md:53-56): the causal
+ * depthwise conv1d of rhz_causal_conv1d (causal_conv1d_step,
+ * delta.rs:232-243; width 4, 3-sample carried state, reset at sequence
+ * starts) over x = the q, k and v projections side by side, C = heads *
+ * (2 d_k + d_v) channels per token (channels [0, H d_k) are q, then k, then
+ * v), followed before any rounding by rhz_gdr_prepare's maps: every q row
+ * l2-normalised and multiplied by q_scale, every k row l2-normalised
+ * (elementwise.rs:125-128), v passed on, beta = sigmoid(beta_logit) and
+ * g = -softplus(a_log[h]) softplus(alpha_logit) (elementwise.rs:5-12,
+ * 36-42).  The outputs are what rhz_gdr_prefill takes with
+ * RHZ_GATE_LOG_ALPHA; they equal rhz_causal_conv1d followed by
+ * rhz_gdr_prepare up to the rounding of the convolved q and k to dtype,
+ * which this pass skips.  bf16 or fp32; d_k and d_v multiples of 8 (bf16)
+ * or 4 (fp32) with d_k / 8 (bf16) or d_k / 4 (fp32) a power of two up to 64
+ * (else RHZ_ERR_UNSUPPORTED: use the two calls); x and the q, k, v outputs
+ * 16-byte aligned and not overlapping.  No counterpart in the reference,
+ * whose steps run one after the other on the CPU. */
+typedef struct rhz_gdr_conv_prepare_args {
+    int32_t batch;    /* dense: B;  packed: number of sequences N (>= 1) */
+    int32_t seq_len;  /* dense: T;  packed: total tokens (>= 0) */
+    int32_t heads;    /* H >= 1 */
+    int32_t d_k;      /* >= 1 */
+    int32_t d_v;      /* >= 1 */
+    int32_t dtype;    /* rhz_dtype of x and of the q, k, v outputs */
+    float q_scale;    /* SPEC.md:53: sqrt(d_k); must be finite */
+    const void* x;              /* [tokens, C] projections, C = H (2 d_k + d_v) */
+    const float* weight;        /* [C, 4] */
+    const float* bias;          /* [C], or NULL for zero */
+    const int32_t* cu_seqlens;  /* [N+1] or NULL (dense) */
+    const float* initial_state; /* [batch, C, 3] conv state, oldest first, or NULL */
+    float* final_state;         /* [batch, C, 3], or NULL */
+    const float* beta_logit;    /* [tokens, H] */
+    const float* alpha_logit;   /* [tokens, H] */
+    const float* a_log;         /* [H] */
+    void* q;                    /* [tokens, H, d_k] out */
+    void* k;                    /* [tokens, H, d_k] out */
+    void* v;                    /* [tokens, H, d_v] out */
+    float* beta;                /* [tokens, H] out */
+    float* g;                   /* [tokens, H] out */
+} rhz_gdr_conv_prepare_args;
+
+rhz_status rhz_gdr_conv_prepare(const rhz_gdr_conv_prepare_args* args, void* stream);
+
 /* RMSNorm of every row of `dim` values with a learned scale, as the
  * per-head norm of the op's output (groupnorm_heads / rmsnorm,
  * norm.rs:8-13, 48-59): y = x / sqrt(mean(x^2) + eps) * scale.  y may alias

@@ -5,9 +5,9 @@ The compute lives in librhizome_gdr.so (hand-written HIP kernels, built by
 end.  Importing the package does not load the library; the first call does,
 and raises if the library is missing.
 """
-from .gdr import (causal_conv1d, decode_step, fp16_range_errors, local_prefill,  # noqa: F401
-                  multistep, philox_fill, prefill, prepare, query_support, rmsnorm_heads,
-                  sync_timeouts)
+from .gdr import (causal_conv1d, conv_prepare, decode_step, fp16_range_errors,  # noqa: F401
+                  local_prefill, multistep, philox_fill, prefill, prepare, query_support,
+                  rmsnorm_heads, sync_timeouts)
 
-__all__ = ["prefill", "local_prefill", "decode_step", "multistep", "causal_conv1d", "prepare",
+__all__ = ["prefill", "local_prefill", "decode_step", "multistep", "causal_conv1d", "prepare", "conv_prepare",
            "rmsnorm_heads", "philox_fill", "query_support", "sync_timeouts", "fp16_range_errors"]

@@ -89,6 +89,17 @@ class PrepareArgs(Structure):
     ]
 
 
+class ConvPrepareArgs(Structure):
+    _fields_ = [
+        ("batch", c_int32), ("seq_len", c_int32), ("heads", c_int32), ("d_k", c_int32),
+        ("d_v", c_int32), ("dtype", c_int32), ("q_scale", c_float),
+        ("x", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("cu_seqlens", c_void_p),
+        ("initial_state", c_void_p), ("final_state", c_void_p),
+        ("beta_logit", c_void_p), ("alpha_logit", c_void_p), ("a_log", c_void_p),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("beta", c_void_p), ("g", c_void_p),
+    ]
+
+
 class RmsnormArgs(Structure):
     _fields_ = [
         ("rows", c_int32), ("dim", c_int32), ("dtype", c_int32), ("eps", c_float),
@@ -150,6 +161,8 @@ def lib():
         L.rhz_causal_conv1d.restype = c_int32
         L.rhz_gdr_prepare.argtypes = [POINTER(PrepareArgs), c_void_p]
         L.rhz_gdr_prepare.restype = c_int32
+        L.rhz_gdr_conv_prepare.argtypes = [POINTER(ConvPrepareArgs), c_void_p]
+        L.rhz_gdr_conv_prepare.restype = c_int32
         L.rhz_rmsnorm_heads.argtypes = [POINTER(RmsnormArgs), c_void_p]
         L.rhz_rmsnorm_heads.restype = c_int32
         L.rhz_philox_fill.argtypes = [c_int32, c_uint64, c_uint64, c_int64, c_int32, c_double,

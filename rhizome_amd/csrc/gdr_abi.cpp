@@ -379,6 +379,53 @@ rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* a, void* stream) {
     return hip_status(rhz::launch_prepare(*a, static_cast<hipStream_t>(stream)), "prepare launch");
 }
 
+rhz_status rhz_gdr_conv_prepare(const rhz_gdr_conv_prepare_args* a, void* stream) {
+    if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
+    if (a->batch < 1) return fail(RHZ_ERR_INVALID_ARG, "batch must be >= 1 (got %d)", a->batch);
+    if (a->seq_len < 0) return fail(RHZ_ERR_INVALID_ARG, "seq_len must be >= 0 (got %d)", a->seq_len);
+    if (a->heads < 1) return fail(RHZ_ERR_INVALID_ARG, "heads must be >= 1 (got %d)", a->heads);
+    if (a->d_k < 1 || a->d_v < 1)
+        return fail(RHZ_ERR_INVALID_ARG, "d_k and d_v must be >= 1 (got %d, %d)", a->d_k, a->d_v);
+    if (a->dtype != RHZ_F32 && a->dtype != RHZ_BF16)
+        return fail(RHZ_ERR_INVALID_ARG, "dtype must be RHZ_F32 or RHZ_BF16 (got %d)", a->dtype);
+    if (!std::isfinite(a->q_scale)) return fail(RHZ_ERR_INVALID_ARG, "q_scale must be finite");
+    if (a->d_k > 512 || a->d_v > 1024)
+        return fail(RHZ_ERR_UNSUPPORTED, "d_k = %d, d_v = %d exceed the supported 512 and 1024", a->d_k, a->d_v);
+    if (!rhz::conv_prepare_supported(a->dtype, a->d_k, a->d_v))
+        return fail(RHZ_ERR_UNSUPPORTED,
+                    "d_k = %d, d_v = %d: need multiples of %d with d_k / %d a power of two up to 64 "
+                    "(use rhz_causal_conv1d and rhz_gdr_prepare)",
+                    a->d_k, a->d_v, a->dtype == RHZ_F32 ? 4 : 8, a->dtype == RHZ_F32 ? 4 : 8);
+    const int64_t C = (int64_t)a->heads * (2 * a->d_k + a->d_v);
+    const int64_t tokens = a->cu_seqlens ? a->seq_len : (int64_t)a->batch * a->seq_len;
+    if (tokens * C > kMaxIndex || (int64_t)a->batch * C * 3 > kMaxIndex)
+        return fail(RHZ_ERR_INVALID_ARG, "tokens * channels and batch * channels * 3 must stay below 2^31");
+    if (!a->weight) return fail(RHZ_ERR_INVALID_ARG, "weight is NULL");
+    if (tokens > 0) {
+        const void* ptrs[] = {a->x, a->q, a->k, a->v, a->beta_logit, a->alpha_logit, a->a_log, a->beta, a->g};
+        const char* names[] = {"x", "q", "k", "v", "beta_logit", "alpha_logit", "a_log", "beta", "g"};
+        for (int i = 0; i < 9; ++i)
+            if (!ptrs[i]) return fail(RHZ_ERR_INVALID_ARG, "%s is NULL", names[i]);
+        for (int i = 0; i < 4; ++i)
+            if (!aligned16(ptrs[i])) return fail(RHZ_ERR_INVALID_ARG, "%s is not 16-byte aligned", names[i]);
+        // x must not overlap an output: every token's outputs are written
+        // while other blocks still read x
+        const size_t es = a->dtype == RHZ_F32 ? 4 : 2;
+        const uintptr_t x0 = reinterpret_cast<uintptr_t>(a->x), x1 = x0 + (size_t)(tokens * C) * es;
+        const size_t nout[] = {(size_t)(tokens * a->heads * a->d_k) * es, (size_t)(tokens * a->heads * a->d_k) * es,
+                               (size_t)(tokens * a->heads * a->d_v) * es};
+        for (int i = 0; i < 3; ++i) {
+            const uintptr_t o0 = reinterpret_cast<uintptr_t>(ptrs[1 + i]), o1 = o0 + nout[i];
+            if (o0 < x1 && x0 < o1) return fail(RHZ_ERR_INVALID_ARG, "%s overlaps x", names[1 + i]);
+        }
+    }
+    if (misaligned(a->weight, 4) || misaligned(a->bias, 4) || misaligned(a->initial_state, 4) ||
+        misaligned(a->final_state, 4) || misaligned(a->cu_seqlens, 4) || misaligned(a->beta_logit, 4) ||
+        misaligned(a->alpha_logit, 4) || misaligned(a->a_log, 4) || misaligned(a->beta, 4) || misaligned(a->g, 4))
+        return fail(RHZ_ERR_INVALID_ARG, "fp32 and int32 tensors must be 4-byte aligned");
+    return hip_status(rhz::launch_conv_prepare(*a, static_cast<hipStream_t>(stream)), "conv prepare launch");
+}
+
 rhz_status rhz_rmsnorm_heads(const rhz_rmsnorm_args* a, void* stream) {
     if (!a) return fail(RHZ_ERR_INVALID_ARG, "args is NULL");
     if (a->rows < 0) return fail(RHZ_ERR_INVALID_ARG, "rows must be >= 0 (got %d)", a->rows);

@@ -8,6 +8,8 @@
 //   prepare_kernel   q, k L2-normalised (q rescaled), beta = sigmoid(logit),
 //                    g = -softplus(a_h) softplus(logit) (elementwise.rs:5-12,
 //                    36-42, 125-128);
+//   conv_prepare_kernel  the two above in one pass over the [q | k | v]
+//                    projections (SPEC.md:53-56);
 //   rmsnorm_kernel   RMSNorm of rows with a learned scale (norm.rs:8-13),
 //                    the per-head norm of the op's output (norm.rs:48-59).
 
@@ -110,17 +112,19 @@ __device__ __forceinline__ int seq_end(const ConvParams& p, int s) {
 
 // Grid: one dimension, block b = (span b / ncb, channel block b % ncb);
 // each thread owns N consecutive channels (one 16-byte access per token
-// when VEC).
-template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, int ncb) {
+// when VEC).  The span's outputs go to emit(t, c, y[N]), called for every
+// token of the span that lies in a sequence, in token order, by every thread
+// of the block at once (the tokens are the block's, so the calls stay
+// converged across the block).
+template <typename T, bool VEC, typename Emit>
+__device__ __forceinline__ void conv_span(const ConvParams& p, int total, int ncb, Emit&& emit) {
     using V = Vec<T, VEC>;
     constexpr int N = V::N;
     const int c = ((blockIdx.x % ncb) * 256 + threadIdx.x) * N;
     const int t0 = (blockIdx.x / ncb) * kConvSpan;
     if (c >= p.C || t0 >= total) return;
     const int t1 = min(t0 + kConvSpan, total);
-    const T* __restrict__ x = static_cast<const T*>(p.x);  // y never overlaps x
-    T* __restrict__ y = static_cast<T*>(p.y);
+    const T* __restrict__ x = static_cast<const T*>(p.x);  // the outputs never overlap x
     const long C = p.C;
     float w[N][4], b[N];
     if (aligned16(p.w)) {  // uniform: one 16-byte load per channel
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
 #pragma unroll
             for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
                 yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
-            V::template store<kConvNT>(y + (t0 + i) * C + c, yt);
+            emit(t0 + i, c, yt);
 #pragma unroll
             for (int e = 0; e < N; ++e) {
                 a[0][e] = a[1][e];
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
 #pragma unroll
         for (int e = 0; e < N; ++e)  // delta.rs:237-238, evaluated left to right
             yt[e] = w[e][0] * a[0][e] + w[e][1] * a[1][e] + w[e][2] * a[2][e] + w[e][3] * xt[e] + b[e];
-        V::template store<kConvNT>(y + t * C + c, yt);
+        emit(t, c, yt);
 #pragma unroll
         for (int e = 0; e < N; ++e) {
             a[0][e] = a[1][e];
@@ -233,6 +237,97 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
                 f[2] = a[2][e];
             }
         }
+    }
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, int ncb) {
+    using V = Vec<T, VEC>;
+    T* __restrict__ y = static_cast<T*>(p.y);
+    const long C = p.C;
+    conv_span<T, VEC>(p, total, ncb, [&](int t, int c, const float (&yt)[V::N]) {
+        V::template store<kConvNT>(y + t * C + c, yt);
+    });
+}
+
+// ------------------------------------------------------- conv1d + prepare
+// The Local block's prologue in one pass: causal conv1d over x = [q | k | v]
+// projections (C = H (2 d_k + d_v) channels per token), then prepare's maps
+// on the convolved values before they are rounded -- q rows l2-normalised
+// and scaled, k rows l2-normalised (elementwise.rs:125-128), v passed on --
+// written as separate q [tokens, H, d_k], k [tokens, H, d_k], v [tokens, H,
+// d_v], with beta = sigmoid(beta_logit) and g = -softplus(a_log[h])
+// softplus(alpha_logit) per (token, head) (elementwise.rs:5-12, 36-42).  A
+// q or k row is G = d_k / N consecutive threads of a block (channel blocks
+// are whole rows), so its sum of squares is a sum over those lanes.
+struct ConvPrepParams {
+    ConvParams conv;
+    void* q;
+    void* k;
+    void* v;
+    const float* beta_logit;
+    const float* alpha_logit;
+    const float* a_log;
+    float* beta;
+    float* g;
+    int heads, d_k, d_v;
+    float q_scale;
+};
+
+template <int G>
+__device__ __forceinline__ float row_sum(float x) {
+    if constexpr (G >= 32) {
+        x = lane_group_sum<16>(x);
+        x += __shfl_xor(x, 16, kWave);
+        if constexpr (G == 64) x += __shfl_xor(x, 32, kWave);
+        return x;
+    } else if constexpr (G > 1) {
+        return lane_group_sum<G>(x);
+    } else {
+        return x;
+    }
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(256) void conv_prepare_kernel(ConvPrepParams p, int total, int ncb) {
+    using V = Vec<T, true>;
+    constexpr int N = V::N;
+    const int H = p.heads, dk = p.d_k, dv = p.d_v;
+    const int qk = H * dk;  // channels of q (and of k)
+    T* __restrict__ qo = static_cast<T*>(p.q);
+    T* __restrict__ ko = static_cast<T*>(p.k);
+    T* __restrict__ vo = static_cast<T*>(p.v);
+    conv_span<T, true>(p.conv, total, ncb, [&](int t, int c, const float (&yt)[N]) {
+        if (c >= 2 * qk) {  // v (uniform over the row's lanes)
+            V::template store<kConvNT>(vo + (long)t * H * dv + (c - 2 * qk), yt);
+            return;
+        }
+        const bool isq = c < qk;
+        const int cc = isq ? c : c - qk;  // channel within q or k
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < N; ++e) ss += yt[e] * yt[e];
+        ss = row_sum<G>(ss);
+        // x / max(||x||, 1e-12) * scale (elementwise.rs:126-127), the
+        // reciprocal norm as v_rsq_f32 of max(||x||^2, 1e-24) (about 1 ulp)
+        const float f = (isq ? p.q_scale : 1.f) * __builtin_amdgcn_rsqf(fmaxf(ss, 1e-24f));
+        float o[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) o[e] = yt[e] * f;
+        V::template store<kRowNT>((isq ? qo : ko) + (long)t * qk + cc, o);
+    });
+    // The gates of the block's (token, head) pairs, one pair per thread: the
+    // blocks holding q channels cover every head once per span.
+    const int cb = (blockIdx.x % ncb) * 256 * N;  // first channel of the block
+    const int t0 = (blockIdx.x / ncb) * kConvSpan;
+    if (cb >= qk || t0 >= total) return;
+    const int h0 = cb / dk, nh = (min(cb + 256 * N, qk) - cb) / dk;
+    const int nt = min(t0 + kConvSpan, total) - t0;
+    for (int i = threadIdx.x; i < nt * nh; i += 256) {
+        const int h = h0 + i % nh;
+        const long r = (long)(t0 + i / nh) * H + h;
+        p.beta[r] = sigmoid_f(p.beta_logit[r]);
+        p.g[r] = -softplus_f(p.a_log[h]) * softplus_f(p.alpha_logit[r]);
     }
 }
 
@@ -459,6 +554,59 @@ hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t st) {
         // one channel per thread, whatever the main kernel's vector width
         const int ecb = (a.channels + 255) / 256;
         hipLaunchKernelGGL(conv1d_empty_kernel, dim3(ecb, min(a.batch, 65535)), dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+bool conv_prepare_supported(int dtype, int d_k, int d_v) {
+    const int n = dtype == RHZ_F32 ? 4 : 8;  // elements per 16-byte access
+    if (d_k % n != 0 || d_v % n != 0) return false;
+    const int g = d_k / n;
+    return g == 1 || g == 2 || g == 4 || g == 8 || g == 16 || g == 32 || g == 64;
+}
+
+hipError_t launch_conv_prepare(const rhz_gdr_conv_prepare_args& a, hipStream_t st) {
+    const int C = a.heads * (2 * a.d_k + a.d_v);
+    ConvPrepParams p{{a.x, a.weight, a.bias, a.cu_seqlens, a.initial_state, a.final_state, nullptr, a.batch,
+                      a.seq_len, C},
+                     a.q, a.k, a.v, a.beta_logit, a.alpha_logit, a.a_log, a.beta, a.g,
+                     a.heads, a.d_k, a.d_v, a.q_scale};
+    const int total = a.cu_seqlens ? a.seq_len : a.batch * a.seq_len;
+    const int n = a.dtype == RHZ_F32 ? 4 : 8;
+    const int g = a.d_k / n;
+    const int ncb = (C / n + 255) / 256;
+    if (total > 0) {
+        const dim3 grid((unsigned)((long)ncb * ((total + kConvSpan - 1) / kConvSpan)));
+#define RHZ_CONV_PREP(T, G) hipLaunchKernelGGL((conv_prepare_kernel<T, G>), grid, dim3(256), 0, st, p, total, ncb)
+        if (a.dtype == RHZ_F32) {
+            switch (g) {
+                case 1: RHZ_CONV_PREP(float, 1); break;
+                case 2: RHZ_CONV_PREP(float, 2); break;
+                case 4: RHZ_CONV_PREP(float, 4); break;
+                case 8: RHZ_CONV_PREP(float, 8); break;
+                case 16: RHZ_CONV_PREP(float, 16); break;
+                case 32: RHZ_CONV_PREP(float, 32); break;
+                default: RHZ_CONV_PREP(float, 64); break;
+            }
+        } else {
+            switch (g) {
+                case 1: RHZ_CONV_PREP(uint16_t, 1); break;
+                case 2: RHZ_CONV_PREP(uint16_t, 2); break;
+                case 4: RHZ_CONV_PREP(uint16_t, 4); break;
+                case 8: RHZ_CONV_PREP(uint16_t, 8); break;
+                case 16: RHZ_CONV_PREP(uint16_t, 16); break;
+                case 32: RHZ_CONV_PREP(uint16_t, 32); break;
+                default: RHZ_CONV_PREP(uint16_t, 64); break;
+            }
+        }
+#undef RHZ_CONV_PREP
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (a.final_state) {
+        const int ecb = (C + 255) / 256;
+        hipLaunchKernelGGL(conv1d_empty_kernel, dim3(ecb, min(a.batch, 65535)), dim3(256), 0, st, p.conv);
         return hipGetLastError();
     }
     return hipSuccess;

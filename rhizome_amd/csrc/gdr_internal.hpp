@@ -53,6 +53,10 @@ hipError_t chunked_range_errors(unsigned int* count, bool reset);
 hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t stream);
 hipError_t launch_prepare(const rhz_gdr_prepare_args& a, hipStream_t stream);
 hipError_t launch_rmsnorm(const rhz_rmsnorm_args& a, hipStream_t stream);
+// conv1d and prepare in one pass; the caller has checked
+// conv_prepare_supported(dtype, d_k, d_v).
+bool conv_prepare_supported(int dtype, int d_k, int d_v);
+hipError_t launch_conv_prepare(const rhz_gdr_conv_prepare_args& a, hipStream_t stream);
 
 // Device Philox-4x32-10 fill.
 hipError_t launch_philox_fill(int kind, uint64_t seed, uint64_t stream_id, int64_t count,

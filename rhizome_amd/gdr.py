@@ -291,6 +291,47 @@ def prepare(q, k, beta_logit, alpha_logit, a_log, *, q_scale=None, q_out=None, k
     return qo, ko, beta, g
 
 
+def conv_prepare(x, weight, bias, beta_logit, alpha_logit, a_log, *, heads, d_k, d_v, q_scale=None,
+                 cu_seqlens=None, initial_state=None, output_final_state=False, q_out=None, k_out=None,
+                 v_out=None, stream=None):
+    """The Local block's prologue in one pass (rhz_gdr_conv_prepare): causal
+    conv1d over x = [q | k | v] projections, then q := l2norm(q) * q_scale
+    (default sqrt(d_k)), k := l2norm(k), beta := sigmoid(beta_logit),
+    g := -softplus(a_log[h]) * softplus(alpha_logit).
+
+    x [B, T, C] (dense) or [tokens, C] with ``cu_seqlens``, C = heads *
+    (2 d_k + d_v); weight [C, 4] fp32; bias [C]; logits [..., heads]; a_log
+    [heads]; initial_state [N, C, 3].  Returns (q, k, v, beta, g,
+    final_state or None) with q, k [..., heads, d_k] and v [..., heads, d_v].
+    """
+    if cu_seqlens is None:
+        B, T, C = x.shape
+        batch, seq_len, lead = B, T, (B, T)
+    else:
+        seq_len, C = x.shape
+        batch, lead = cu_seqlens.numel() - 1, (seq_len,)
+    if C != heads * (2 * d_k + d_v):
+        raise ValueError(f"x has {C} channels, not heads * (2 d_k + d_v) = {heads * (2 * d_k + d_v)}")
+    if tuple(weight.shape) != (C, 4) or weight.dtype != torch.float32:
+        raise ValueError("weight must be fp32 [C, 4]")
+    q = q_out if q_out is not None else torch.empty(lead + (heads, d_k), dtype=x.dtype, device=x.device)
+    k = k_out if k_out is not None else torch.empty(lead + (heads, d_k), dtype=x.dtype, device=x.device)
+    v = v_out if v_out is not None else torch.empty(lead + (heads, d_v), dtype=x.dtype, device=x.device)
+    beta = torch.empty(lead + (heads,), dtype=torch.float32, device=x.device)
+    g = torch.empty_like(beta)
+    fin = torch.empty((batch, C, 3), dtype=torch.float32, device=x.device) if output_final_state else None
+    a = _abi.ConvPrepareArgs()
+    a.batch, a.seq_len, a.heads, a.d_k, a.d_v = batch, seq_len, heads, d_k, d_v
+    a.dtype = _DTYPES[x.dtype]
+    a.q_scale = float(d_k) ** 0.5 if q_scale is None else float(q_scale)
+    a.x, a.weight, a.bias = _ptr(x), _ptr(weight), _ptr(bias)
+    a.cu_seqlens, a.initial_state, a.final_state = _ptr(cu_seqlens), _ptr(initial_state), _ptr(fin)
+    a.beta_logit, a.alpha_logit, a.a_log = _ptr(beta_logit), _ptr(alpha_logit), _ptr(a_log)
+    a.q, a.k, a.v, a.beta, a.g = _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g)
+    _abi.check(_abi.lib().rhz_gdr_conv_prepare(byref(a), _stream(stream)))
+    return q, k, v, beta, g, fin
+
+
 def rmsnorm_heads(x, scale, eps: float = 1e-6, *, out=None, stream=None):
     """RMSNorm over the last dimension with a learned scale (norm.rs:8-13, 48-59)."""
     dim = x.shape[-1]

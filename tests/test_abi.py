@@ -295,6 +295,42 @@ def test_conv1d_validation(over, msg):
     assert msg in _abi.last_error()
 
 
+def _convprep(**over):
+    a = _abi.ConvPrepareArgs()
+    a.batch, a.seq_len, a.heads, a.d_k, a.d_v = 4, 4096, 16, 128, 128
+    a.dtype, a.q_scale = _abi.BF16, 11.3
+    a.x = A
+    # outputs at distinct fake addresses, far from x (validation only: every
+    # case below fails before any HIP call)
+    a.q, a.k, a.v = 1 << 36, 2 << 36, 3 << 36
+    for name in ("weight", "beta_logit", "alpha_logit", "a_log", "beta", "g"):
+        setattr(a, name, A)
+    for key, val in over.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(batch=0), _abi.ERR_INVALID_ARG, "batch"), (dict(seq_len=-1), _abi.ERR_INVALID_ARG, "seq_len"),
+    (dict(heads=0), _abi.ERR_INVALID_ARG, "heads"), (dict(d_k=0), _abi.ERR_INVALID_ARG, "d_k and d_v"),
+    (dict(dtype=_abi.F64), _abi.ERR_INVALID_ARG, "dtype"),
+    (dict(q_scale=float("inf")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
+    (dict(d_k=96), _abi.ERR_UNSUPPORTED, "power of two"), (dict(d_v=12), _abi.ERR_UNSUPPORTED, "multiples of 8"),
+    (dict(dtype=_abi.F32, d_k=48), _abi.ERR_UNSUPPORTED, "multiples of 4"),
+    (dict(d_k=1024), _abi.ERR_UNSUPPORTED, "512"),
+    (dict(weight=None), _abi.ERR_INVALID_ARG, "weight is NULL"), (dict(x=None), _abi.ERR_INVALID_ARG, "x is NULL"),
+    (dict(g=None), _abi.ERR_INVALID_ARG, "g is NULL"),
+    (dict(q=(1 << 36) + 8), _abi.ERR_INVALID_ARG, "q is not 16-byte aligned"),
+    (dict(v=A), _abi.ERR_INVALID_ARG, "v overlaps x"),
+    (dict(k=A + 4 * 4096 * 16 * 384 * 2 - 16), _abi.ERR_INVALID_ARG, "k overlaps x"),
+    (dict(bias=A + 2), _abi.ERR_INVALID_ARG, "4-byte"),
+    (dict(seq_len=1 << 20), _abi.ERR_INVALID_ARG, "2^31"),
+])
+def test_conv_prepare_validation(over, status, msg):
+    assert _abi.lib().rhz_gdr_conv_prepare(byref(_convprep(**over)), None) == status
+    assert msg in _abi.last_error()
+
+
 def _prep(**over):
     a = _abi.PrepareArgs()
     a.tokens, a.heads, a.d_k, a.dtype, a.q_scale = 16384, 16, 128, _abi.BF16, 11.3

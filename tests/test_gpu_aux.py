@@ -222,6 +222,130 @@ def test_local_prefill_matches_prepare_then_prefill(device, shape, with_state):
           f"prepare -> prefill normwise {sep:.3g}", flush=True)
 
 
+def _conv_prepare_case(device, rng, lengths, H, dk, dv, dtype, with_state):
+    """Inputs of one rhz_gdr_conv_prepare case and the oracle's conv1d -> prepare."""
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    n_tok, n = int(cu[-1]), len(lengths)
+    C = H * (2 * dk + dv)
+    x, x64 = to_device(rng.normal(size=(n_tok, C)), dtype, device)
+    w, w64 = to_device(rng.normal(scale=0.5, size=(C, 4)), torch.float32, device)
+    b, b64 = to_device(rng.normal(scale=0.1, size=C), torch.float32, device)
+    bl, bl64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    al, al64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    a, a64 = to_device(rng.normal(size=H), torch.float32, device)
+    init = init64 = None
+    if with_state:
+        init, init64 = to_device(rng.normal(size=(n, C, 3)), torch.float32, device)
+    ry, rf = O.conv1d_batched(cu, x64, w64, b64, init64)
+    qk = H * dk
+    rq, rk, rb, rg = O.prepare(ry[:, :qk].reshape(n_tok, H, dk), ry[:, qk:2 * qk].reshape(n_tok, H, dk),
+                               bl64, al64, a64, float(dk) ** 0.5)
+    rv = ry[:, 2 * qk:].reshape(n_tok, H, dv)
+    dev = dict(x=x, w=w, b=b, bl=bl, al=al, a=a, init=init,
+               cu=torch.from_numpy(cu.astype(np.int32)).to(device))
+    return dev, (rq, rk, rv, rb, rg, rf)
+
+
+@pytest.mark.parametrize("dtype,tol", PATHS)
+@pytest.mark.parametrize("lengths,H,dk,dv,with_state", [
+    ([100, 100], 2, 128, 128, False),
+    ([0, 1, 2, 3, 31, 32, 33, 0, 200], 3, 64, 96, True),     # empty and short sequences, span edges
+    ([300, 17], 4, 32, 256, True),
+    ([0, 5, 0, 17, 1, 0], 16, 128, 128, True),
+    ([0, 0, 0], 2, 128, 64, True),                          # zero tokens, final states only
+    ([513], 1, 8 * 64, 8, False),                            # the widest q/k rows (bf16: 64 lanes)
+])
+def test_conv_prepare(device, dtype, tol, lengths, H, dk, dv, with_state):
+    """rhz_gdr_conv_prepare against the oracle's causal_conv1d_step
+    (delta.rs:232-243) along packed sequences followed by prepare
+    (elementwise.rs:5-12, 36-42, 125-128; SPEC.md:53-56)."""
+    if dtype == torch.float32 and dk == 512:
+        pytest.skip("fp32 rows of 512 need 128 lanes; the ABI takes up to 64")
+    rng = _rng(77 + len(lengths) + dk)
+    d, ref = _conv_prepare_case(device, rng, lengths, H, dk, dv, dtype, with_state)
+    rq, rk, rv, rb, rg, rf = ref
+    q, k, v, beta, g, fin = rhizome_amd.conv_prepare(d["x"], d["w"], d["b"], d["bl"], d["al"], d["a"], heads=H,
+                                                     d_k=dk, d_v=dv, cu_seqlens=d["cu"], initial_state=d["init"],
+                                                     output_final_state=True)
+    torch.cuda.synchronize()
+    n_tok = sum(lengths)
+    if n_tok:
+        mq = check_close(q.double().cpu().numpy(), rq, tol, "conv prepare q")
+        check_close(k.double().cpu().numpy(), rk, tol, "conv prepare k")
+        check_close(v.double().cpu().numpy(), rv, tol, "conv prepare v")
+        check_close(beta.double().cpu().numpy(), rb, F32_TOL, "conv prepare beta")
+        check_close(g.double().cpu().numpy(), rg, F32_TOL, "conv prepare g")
+    else:
+        mq = None
+    mf = check_close(fin.cpu().numpy(), rf, F32_TOL, "conv prepare final conv state")
+    print(f"conv prepare {lengths[:4]}.. H={H} d_k={dk} d_v={dv} {dtype}: q {mq} final {mf}", flush=True)
+
+
+def test_conv_prepare_dense_equals_packed_and_chain(device):
+    """Dense and packed calls agree bit for bit, and the pass equals the device's
+    own conv1d -> prepare where that chain does not round in between (fp32)."""
+    rng = _rng(91)
+    B, T, H, dk, dv = 2, 150, 2, 64, 64
+    C = H * (2 * dk + dv)
+    x = torch.from_numpy(rng.normal(size=(B, T, C)).astype(np.float32)).to(device)
+    w = torch.from_numpy(rng.normal(scale=0.5, size=(C, 4)).astype(np.float32)).to(device)
+    bl = torch.from_numpy(rng.normal(size=(B, T, H)).astype(np.float32)).to(device)
+    al = torch.from_numpy(rng.normal(size=(B, T, H)).astype(np.float32)).to(device)
+    a = torch.from_numpy(rng.normal(size=H).astype(np.float32)).to(device)
+    d1 = rhizome_amd.conv_prepare(x, w, None, bl, al, a, heads=H, d_k=dk, d_v=dv, output_final_state=True)
+    cu = torch.tensor([0, T, 2 * T], dtype=torch.int32, device=device)
+    d2 = rhizome_amd.conv_prepare(x.view(B * T, C), w, None, bl.view(B * T, H), al.view(B * T, H), a, heads=H,
+                                  d_k=dk, d_v=dv, cu_seqlens=cu, output_final_state=True)
+    torch.cuda.synchronize()
+    for u, z in zip(d1, d2):
+        assert torch.equal(u.reshape(-1), z.reshape(-1))
+    y, fin = rhizome_amd.causal_conv1d(x, w, output_final_state=True)
+    qk = H * dk
+    q2, k2, beta2, g2 = rhizome_amd.prepare(y[..., :qk].contiguous().view(B, T, H, dk),
+                                            y[..., qk:2 * qk].contiguous().view(B, T, H, dk), bl, al, a)
+    torch.cuda.synchronize()
+    assert torch.equal(fin, d1[5])
+    assert torch.equal(y[..., 2 * qk:].reshape(B, T, H, dv), d1[2])
+    assert torch.allclose(q2, d1[0], rtol=1e-5, atol=1e-6) and torch.allclose(k2, d1[1], rtol=1e-5, atol=1e-6)
+    assert torch.equal(beta2, d1[3]) and torch.equal(g2, d1[4])
+
+
+def test_local_chain_through_conv_prepare(device):
+    """The Local block with its prologue in one pass: rhz_gdr_conv_prepare ->
+    rhz_gdr_prefill (chunked) -> rhz_rmsnorm_heads, each stage reading the
+    previous one's device output, against the oracle's conv1d -> prepare ->
+    prefill -> rmsnorm on the same raw inputs."""
+    rng = _rng(97)
+    lengths, H, dk, dv = [0, 130, 64, 300, 1], 4, 128, 128
+    d, ref = _conv_prepare_case(device, rng, lengths, H, dk, dv, torch.bfloat16, True)
+    rq, rk, rv, rb, rg, _ = ref
+    q, k, v, beta, g, _ = rhizome_amd.conv_prepare(d["x"], d["w"], d["b"], d["bl"], d["al"], d["a"], heads=H,
+                                                   d_k=dk, d_v=dv, cu_seqlens=d["cu"], initial_state=d["init"])
+    o, fin = rhizome_amd.prefill(q, k, v, g, beta, cu_seqlens=d["cu"], algo="chunked")
+    s, s64 = to_device(rng.normal(size=dv), torch.float32, device)
+    n_tok = sum(lengths)
+    y = rhizome_amd.rmsnorm_heads(o.view(n_tok * H, dv), s, 1e-6)
+    torch.cuda.synchronize()
+    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    # each stage against the oracle on that stage's device input
+    check_close(q.double().cpu().numpy(), rq, BF16_TOL, "chain conv prepare q")
+    check_close(k.double().cpu().numpy(), rk, BF16_TOL, "chain conv prepare k")
+    dq, dk_, dv_ = (t.double().cpu().numpy() for t in (q, k, v))
+    db, dg = beta.double().cpu().numpy(), g.double().cpu().numpy()
+    ro, rf = O.prefill_batched(cu, dq, dk_, dv_, np.exp(dg), db, None)
+    mo = check_close(o.double().cpu().numpy(), ro, BF16_TOL, "chain prefill o")
+    check_close(fin.cpu().numpy(), rf, BF16_TOL, "chain prefill final state")
+    ry = O.rmsnorm_rows(o.double().cpu().numpy().reshape(n_tok * H, dv), s64, 1e-6)
+    my = check_close(y.double().cpu().numpy(), ry, BF16_TOL, "chain rmsnorm")
+    # end to end against the oracle's chain on the raw inputs (reported: the
+    # prepared q and k are rounded to bf16 on the way through HBM, as after
+    # rhz_gdr_prepare)
+    ro2, _ = O.prefill_batched(cu, rq, rk, rv, np.exp(rg), rb, None)
+    e2e = float(np.linalg.norm(o.double().cpu().numpy() - ro2) / max(np.linalg.norm(ro2), 1e-300))
+    print(f"local chain through conv_prepare: o {mo} rmsnorm {my}; end-to-end o normwise {e2e:.3g}", flush=True)
+
+
 def test_local_prefill_config1_shape(device):
     """rhz_gdr_local_prefill at the size it is benchmarked on (B=4, H=16,
     T=4096, d=128, raw projections and logits as the bench draws them)
