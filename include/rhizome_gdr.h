@@ -63,16 +63,20 @@ typedef enum rhz_gate { RHZ_GATE_LOG_ALPHA = 0, RHZ_GATE_ALPHA = 1 } rhz_gate;
  * RECURRENT: token-sequential fp32 recurrence (the fp32-input path).
  * CHUNKED:   64-token chunks, WY/UT transform on fp16 MFMA with fp32
  *            accumulation and fp32 state (bf16 inputs only, converted to
- *            fp16 on chip).  q and k are expected L2-normalised, as the
- *            reference's op takes them (delta.rs:17), so that their
- *            elements and inner products lie within fp16's range
- *            (|x| < 65520); the state and the corrected values U are
- *            rescaled by powers of two and have no such limit.  Launches
- *            that meet q, k or products beyond that range, or non-finite
- *            q or k, are counted by rhz_gdr_fp16_range_errors: their
- *            results are not to be trusted, and RECURRENT takes such
- *            inputs.  A log-decay at or below -80 (alpha <= 1.8e-35) is
- *            taken as alpha = 0: the past is forgotten exactly. */
+ *            fp16 on chip).  The op's domain is the reference's: q
+ *            L2-normalised and scaled, k L2-normalised (delta.rs:17-20;
+ *            SPEC.md:53 scales q by sqrt(d_k)), so that q and k elements
+ *            and their inner products are bounded by q's scale, far inside
+ *            fp16's range (|x| < 65520); the state and the corrected values
+ *            U are rescaled by powers of two and have no such limit.
+ *            Launches that meet q, k or products beyond that range, or
+ *            non-finite q or k, are counted by rhz_gdr_fp16_range_errors:
+ *            their results are not to be trusted, and RECURRENT (fp32
+ *            arithmetic on the same bf16 values) takes such inputs.  The
+ *            fused entry points normalise q and k themselves and stay in
+ *            range (rhz_gdr_local_prefill, rhz_gdr_conv_prepare).  A
+ *            log-decay at or below -80 (alpha <= 1.8e-35) is taken as
+ *            alpha = 0: the past is forgotten exactly. */
 typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUNKED = 2 } rhz_algo;
 
 /* Op identities for rhz_gdr_query_support, named after the plan-level ops
@@ -304,8 +308,12 @@ rhz_status rhz_gdr_prepare(const rhz_gdr_prepare_args* args, void* stream);
  * through HBM.  The result is rhz_gdr_prepare followed by rhz_gdr_prefill up
  * to that rounding.  bf16 and the CHUNKED algorithm only (AUTO resolves to
  * it; anything else is RHZ_ERR_UNSUPPORTED); the workspace is the one
- * rhz_gdr_prefill_workspace_size reports for `prefill`.  No counterpart in
- * the reference, whose steps run one after the other on the CPU. */
+ * rhz_gdr_prefill_workspace_size reports for `prefill`.  Because q and k
+ * are normalised on chip, every fp16 operand the kernel forms from them is
+ * bounded by |q_scale|, which must be at most 2^15 (else
+ * RHZ_ERR_UNSUPPORTED): any finite projections are in range.  No
+ * counterpart in the reference, whose steps run one after the other on the
+ * CPU. */
 typedef struct rhz_gdr_local_args {
     rhz_gdr_prefill_args prefill;
     float q_scale;             /* SPEC.md:53: sqrt(d_k); must be finite */

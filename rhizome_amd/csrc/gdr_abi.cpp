@@ -203,6 +203,12 @@ rhz_status rhz_gdr_local_prefill(const rhz_gdr_local_args* args, void* stream) {
     if (algo != RHZ_ALGO_CHUNKED)
         return fail(RHZ_ERR_UNSUPPORTED, "the fused prologue runs on the CHUNKED path only (bf16, d_k 8..128)");
     if (!std::isfinite(args->q_scale)) return fail(RHZ_ERR_INVALID_ARG, "q_scale must be finite");
+    // the prepared q has elements of at most |q_scale| and q.k products of at
+    // most |q_scale| (unit rows), so this bound keeps every fp16 operand the
+    // kernel forms from q and k in range whatever the raw projections hold
+    if (!(std::fabs(args->q_scale) <= 32768.f))
+        return fail(RHZ_ERR_UNSUPPORTED, "|q_scale| above 2^15 would take the chunked kernel's fp16 operands out of "
+                                         "range; use rhz_gdr_prepare and RHZ_ALGO_RECURRENT");
     const int64_t tokens = a.cu_seqlens ? (int64_t)a.seq_len : (int64_t)a.batch * a.seq_len;
     if (tokens > 0) {
         if (!args->beta_logit) return fail(RHZ_ERR_INVALID_ARG, "beta_logit is NULL");

@@ -148,6 +148,9 @@ def _local(**over):
     (dict(a_log=A + 2), _abi.ERR_INVALID_ARG, "a_log must be 4-byte aligned"),
     (dict(q_scale=float("nan")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
     (dict(q_scale=float("inf")), _abi.ERR_INVALID_ARG, "q_scale must be finite"),
+    # beyond 2^15 the prepared q could leave the kernel's fp16 range
+    (dict(q_scale=40000.0), _abi.ERR_UNSUPPORTED, "2^15"),
+    (dict(q_scale=-32768.5), _abi.ERR_UNSUPPORTED, "2^15"),
     (dict(q=None), _abi.ERR_INVALID_ARG, "q is NULL"),
     (dict(k=A + 8), _abi.ERR_INVALID_ARG, "16-byte aligned"),
     (dict(beta_logit=A + 1), _abi.ERR_INVALID_ARG, "4-byte aligned"),

@@ -378,6 +378,56 @@ def test_local_prefill_config1_shape(device):
     print(f"local prefill at B=4 H=16 T=4096 d=128: o {mo} final {mf}", flush=True)
 
 
+@pytest.mark.parametrize("big", [7e4, 1e15])
+def test_fused_prologues_take_large_projections(device, big):
+    """Projections far beyond fp16's range (the plain chunked path's limit):
+    both fused entry points normalise q and k before any fp16 operand is
+    formed, so they match the oracle with no range error."""
+    rng = _rng(61)
+    lengths, H, dk, dv = [70, 130], 2, 64, 64
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    n_tok = int(cu[-1])
+    qr = rng.normal(size=(n_tok, H, dk))
+    kr = rng.normal(size=(n_tok, H, dk))
+    qr[5, 0, 3] = big
+    qr[100, 1, :] *= big
+    kr[7, 1, 10] = -big
+    q, q64 = to_device(qr, torch.bfloat16, device)
+    k, k64 = to_device(kr, torch.bfloat16, device)
+    v, v64 = to_device(rng.normal(size=(n_tok, H, dv)), torch.bfloat16, device)
+    bl, bl64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    al, al64 = to_device(rng.normal(size=(n_tok, H)), torch.float32, device)
+    a, a64 = to_device(rng.normal(size=H), torch.float32, device)
+    cu_dev = torch.from_numpy(cu.astype(np.int32)).to(device)
+    scale = float(dk) ** 0.5
+    rq, rk, rb, rg = O.prepare(q64, k64, bl64, al64, a64, scale)
+    ro, rf = O.prefill_batched(cu, rq, rk, v64, np.exp(rg), rb, None)
+    rhizome_amd.fp16_range_errors()  # reset
+    o, fin = rhizome_amd.local_prefill(q, k, v, bl, al, a, q_scale=scale, cu_seqlens=cu_dev)
+    torch.cuda.synchronize()
+    assert rhizome_amd.fp16_range_errors() == 0 and rhizome_amd.sync_timeouts() == 0
+    check_close(o.double().cpu().numpy(), ro, BF16_TOL, f"fused prologue o, element {big:g}")
+    check_close(fin.cpu().numpy(), rf, BF16_TOL, f"fused prologue final state, element {big:g}")
+    # the one-pass conv1d + prepare, with an identity conv (weight [0, 0, 0, 1])
+    x = torch.cat([q.view(n_tok, H * dk), k.view(n_tok, H * dk), v.view(n_tok, H * dv)], dim=1).contiguous()
+    C = x.shape[1]
+    w = torch.zeros((C, 4), dtype=torch.float32, device=device)
+    w[:, 3] = 1.0
+    qp, kp, vp, beta, g, _ = rhizome_amd.conv_prepare(x, w, None, bl, al, a, heads=H, d_k=dk, d_v=dv,
+                                                      cu_seqlens=cu_dev)
+    o2, fin2 = rhizome_amd.prefill(qp, kp, vp, g, beta, cu_seqlens=cu_dev, algo="chunked")
+    torch.cuda.synchronize()
+    assert rhizome_amd.fp16_range_errors() == 0 and rhizome_amd.sync_timeouts() == 0
+    # stage by stage: the prepared q, k against the oracle's prepare, the
+    # prefill against the oracle on those (bf16) values
+    check_close(qp.double().cpu().numpy(), rq, BF16_TOL, f"conv prepare q, element {big:g}")
+    check_close(kp.double().cpu().numpy(), rk, BF16_TOL, f"conv prepare k, element {big:g}")
+    ro2, rf2 = O.prefill_batched(cu, qp.double().cpu().numpy(), kp.double().cpu().numpy(), v64,
+                                 np.exp(g.double().cpu().numpy()), beta.double().cpu().numpy(), None)
+    check_close(o2.double().cpu().numpy(), ro2, BF16_TOL, f"conv prepare -> prefill o, element {big:g}")
+    check_close(fin2.cpu().numpy(), rf2, BF16_TOL, f"conv prepare -> prefill final state, element {big:g}")
+
+
 def test_local_prefill_is_deterministic_and_rejects_fp32(device):
     rng = _rng(41)
     H, dk, dv, T = 2, 64, 64, 200

@@ -62,6 +62,22 @@ def test_shapes(device, algo, dtype, tol, shape):
     _check(w, o, fin, tol, tag=f"{shape} {algo} {dtype}")
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, F32_TOL), (torch.bfloat16, BF16_TOL)])
+@pytest.mark.parametrize("shape", [
+    # the recurrent path's two kernels: positions staged through LDS (d_k <=
+    # 128, d_v a multiple of 4) and loaded one position ahead (the rest)
+    dict(lengths=[0, 70, 1, 33], d_k=256, d_v=64),    # d_k past 128: 16 lanes per row
+    dict(lengths=[65, 0, 40], d_k=200, d_v=24),
+    dict(lengths=[100, 3], d_k=64, d_v=6),            # d_v not a multiple of 4
+    dict(lengths=[31, 32, 33, 97], d_k=128, d_v=36),  # blocks of 32 positions, partial last block
+])
+def test_recurrent_kernels(device, dtype, tol, shape):
+    w = Prefill(heads=2, d_k=shape["d_k"], d_v=shape["d_v"], lengths=shape["lengths"], dtype=dtype,
+                device=device, state_std=0.02)
+    o, fin = w.run(algo="recurrent")
+    _check(w, o, fin, tol, tag=f"recurrent {shape} {dtype}")
+
+
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)
 def test_varlen_with_edges(device, algo, dtype, tol):
     # empty, single-token, chunk-boundary and ragged sequences in one pack
