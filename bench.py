@@ -122,7 +122,7 @@ PROFILES = {
     "prepare": "prepare_kernel_bf16_t16384_h16_d128.md",
     "rmsnorm": "rmsnorm_kernel_bf16_rows262144_d128.md",
     "local": "gdr_chunk_kernel_128_pro_local_b4_h16_t4096_d128.md",
-    "prefill_fp32": "gdr_recurrent_kernel_prefill_fp32_b4_h16_t4096_d128.md",
+    "prefill_fp32": "gdr_staged_recurrent_kernel_prefill_fp32_b4_h16_t4096_d128.md",
     "conv_prepare": "conv_prepare_kernel_bf16_t16384_h16_d128.md",
 }
 
@@ -271,8 +271,9 @@ def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
 
 def bench_prefill_fp32(torch, steps, warmup) -> dict:
     """The fp32-input path on the headline prefill shape: rhz_gdr_prefill with
-    fp32 q/k/v/o and RHZ_ALGO_RECURRENT (gdr_recurrent_kernel, token by token,
-    one wave per 8 state rows of a head)."""
+    fp32 q/k/v/o and RHZ_ALGO_RECURRENT (gdr_staged_recurrent_kernel, token by
+    token, one wave per 8 state rows of a head, four waves sharing each
+    32-position block of k, q, gates and k.q staged through LDS)."""
     import rhizome_amd
     from rhizome_amd import _abi, gdr
 
@@ -319,7 +320,7 @@ def bench_prefill_fp32(torch, steps, warmup) -> dict:
                         "waves": B * H * ((dv + 7) // 8)},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles("prefill_fp32"),
-                         "kernel": "gdr_recurrent_kernel<8,true,float>", "algorithmic_bytes": nbytes,
+                         "kernel": "gdr_staged_recurrent_kernel<8,float>", "algorithmic_bytes": nbytes,
                          "launch_us": ms * 1e3,
                          "fp32_valu": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": PEAK_FP32_TFLOPS,
                                        "unit": "TFLOP/s",
