@@ -242,6 +242,8 @@ def bench_prefill(torch, steps, warmup, c=None):
         raise RuntimeError("a chunked-kernel LDS wait gave up during the benchmark")
     if rhizome_amd.fp16_range_errors() != 0:
         raise RuntimeError("a chunked-kernel fp16 operand was out of range during the benchmark")
+    if rhizome_amd.exact_reruns() != 0:
+        raise RuntimeError("chunked-kernel workgroups took the exact rerun during the benchmark")
     flops = prefill_flops(lengths, H, dk, dv)
     algo_bytes = prefill_bytes(n_tok, H, dk, dv, n_seq, init_state=init is not None)
     host = {"q": q, "k": k, "v": v, "g": g, "beta": beta, "tokens": n_tok, **info}
@@ -535,7 +537,7 @@ def bench_local(torch, steps, warmup):
         for _ in range(warmup):
             fn()
         out[name] = {"ms_per_step": time_region(torch, stream, fn, steps), **info}
-    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0:
+    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0 or rhizome_amd.exact_reruns() != 0:
         raise RuntimeError("a chunked-kernel diagnostic counter is nonzero after the Local-block leg")
     tokens = B * T
     # raw q, k, v read and o written once (bf16), two fp32 logits per
@@ -649,7 +651,7 @@ def bench_local_chain(torch, steps, warmup):
             fn()
         ms = time_region(torch, stream, fn, steps)
         out[name] = {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), **info}
-    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0:
+    if rhizome_amd.sync_timeouts() != 0 or rhizome_amd.fp16_range_errors() != 0 or rhizome_amd.exact_reruns() != 0:
         raise RuntimeError("a chunked-kernel diagnostic counter is nonzero after the Local-block chain leg")
     best = min(out, key=lambda n: out[n]["ms_per_step"])
     return {"metric": "Local-block mixer tokens/s (conv1d + prepare + GDR prefill + per-head RMSNorm)",

@@ -63,20 +63,21 @@ typedef enum rhz_gate { RHZ_GATE_LOG_ALPHA = 0, RHZ_GATE_ALPHA = 1 } rhz_gate;
  * RECURRENT: token-sequential fp32 recurrence (the fp32-input path).
  * CHUNKED:   64-token chunks, WY/UT transform on fp16 MFMA with fp32
  *            accumulation and fp32 state (bf16 inputs only, converted to
- *            fp16 on chip).  The op's domain is the reference's: q
- *            L2-normalised and scaled, k L2-normalised (delta.rs:17-20;
- *            SPEC.md:53 scales q by sqrt(d_k)), so that q and k elements
- *            and their inner products are bounded by q's scale, far inside
- *            fp16's range (|x| < 65520); the state and the corrected values
- *            U are rescaled by powers of two and have no such limit.
- *            Launches that meet q, k or products beyond that range, or
- *            non-finite q or k, are counted by rhz_gdr_fp16_range_errors:
- *            their results are not to be trusted, and RECURRENT (fp32
- *            arithmetic on the same bf16 values) takes such inputs.  The
- *            fused entry points normalise q and k themselves and stay in
- *            range (rhz_gdr_local_prefill, rhz_gdr_conv_prepare).  A
- *            log-decay at or below -80 (alpha <= 1.8e-35) is taken as
- *            alpha = 0: the past is forgotten exactly. */
+ *            fp16 on chip).  The state and the corrected values U are
+ *            rescaled by powers of two.  The operands formed from q and k
+ *            are accurate in the reference's domain (delta.rs:17-20: k
+ *            L2-normalised, beta and alpha in [0, 1]; q L2-normalised and
+ *            scaled, SPEC.md:53), and the kernel checks it chunk by chunk: a
+ *            workgroup that meets a key row with |k|^2 > 1.03125, a beta or
+ *            alpha outside [0, 1] or NaN, or an fp16 entry of beta K K^T or
+ *            Q K^T (with their decays) that is not finite or of magnitude
+ *            65520 or more, recomputes its rows of the state with the fp32
+ *            recurrence of RECURRENT inside the same launch.  Every finite
+ *            input therefore gets the recurrence's result; such reruns are
+ *            slower and are counted by rhz_gdr_exact_reruns.  q elements
+ *            below 2^-14 in magnitude are held to 2^-25 absolute (fp16
+ *            subnormals).  A log-decay at or below -80 (alpha <= 1.8e-35)
+ *            is taken as alpha = 0: the past is forgotten exactly. */
 typedef enum rhz_algo { RHZ_ALGO_AUTO = 0, RHZ_ALGO_RECURRENT = 1, RHZ_ALGO_CHUNKED = 2 } rhz_algo;
 
 /* Op identities for rhz_gdr_query_support, named after the plan-level ops
@@ -219,16 +220,27 @@ rhz_status rhz_gdr_prefill_noalloc(const rhz_gdr_prefill_args* args, void* strea
  * last reset may have produced wrong results. */
 rhz_status rhz_gdr_sync_timeouts(uint32_t* count, int32_t reset);
 
-/* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
- * reference, whose op computes in f32 throughout): the number of
- * (workgroup, wave) pairs, counted once per launch, since the last reset
- * whose fp16 MFMA operands formed from q and k on chip -- the blocks of
- * beta K K^T and Q K^T with their decays -- held a NaN, an infinity or a
- * value of magnitude 65520 or more in any chunk.  That happens for q or k elements or inner
- * products beyond fp16's range and for non-finite q or k; a nonzero count
- * means that some chunked launch since the last reset may have produced
- * wrong results.  Same calling convention as rhz_gdr_sync_timeouts. */
+/* Diagnostics of the fused-prologue chunked kernel, rhz_gdr_local_prefill
+ * (no counterpart in the reference, whose op computes in f32 throughout):
+ * the number of (workgroup, wave) pairs, counted once per launch, since the
+ * last reset whose fp16 MFMA operands formed from q and k on chip -- the
+ * blocks of beta K K^T and Q K^T with their decays -- held a NaN, an
+ * infinity or a value of magnitude 65520 or more in any chunk.  Its q and k
+ * rows are normalised on chip and |q_scale| <= 2^15, so only non-finite
+ * projections do that; a nonzero count means that some such launch since
+ * the last reset may have produced wrong results.  The plain CHUNKED path
+ * recomputes such workgroups exactly instead (rhz_gdr_exact_reruns) and
+ * adds nothing here.  Same calling convention as rhz_gdr_sync_timeouts. */
 rhz_status rhz_gdr_fp16_range_errors(uint32_t* count, int32_t reset);
+
+/* Diagnostics of the CHUNKED prefill kernel (no counterpart in the
+ * reference): the number of workgroups -- one per 32 state rows of a
+ * (sequence, head) -- since the last reset whose inputs left the domain of
+ * the fp16 operands (see rhz_algo) and which recomputed their rows with the
+ * fp32 recurrence in the same launch.  Their results are the recurrence's;
+ * a nonzero count only means those launches ran slower.  Same calling
+ * convention as rhz_gdr_sync_timeouts. */
+rhz_status rhz_gdr_exact_reruns(uint32_t* count, int32_t reset);
 
 /* Test hook (no counterpart in the reference): rhz_gdr_prefill with the
  * CHUNKED kernel's waits bounded at spin_limit polls (>= 1) instead of the

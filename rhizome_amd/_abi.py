@@ -151,6 +151,8 @@ def lib():
         L.rhz_gdr_sync_timeouts.restype = c_int32
         L.rhz_gdr_fp16_range_errors.argtypes = [POINTER(c_uint32), c_int32]
         L.rhz_gdr_fp16_range_errors.restype = c_int32
+        L.rhz_gdr_exact_reruns.argtypes = [POINTER(c_uint32), c_int32]
+        L.rhz_gdr_exact_reruns.restype = c_int32
         L.rhz_gdr_prefill_spin_limit.argtypes = [POINTER(PrefillArgs), c_int32, c_void_p]
         L.rhz_gdr_prefill_spin_limit.restype = c_int32
         L.rhz_gdr_decode_step.argtypes = [POINTER(DecodeArgs), c_void_p]

@@ -238,6 +238,15 @@ rhz_status rhz_gdr_fp16_range_errors(uint32_t* count, int32_t reset) {
     return ok();
 }
 
+rhz_status rhz_gdr_exact_reruns(uint32_t* count, int32_t reset) {
+    if (!count) return fail(RHZ_ERR_INVALID_ARG, "count is NULL");
+    unsigned int n = 0;
+    const hipError_t e = rhz::chunked_exact_reruns(&n, reset != 0);
+    if (e != hipSuccess) return hip_status(e, "reading the exact rerun count");
+    *count = n;
+    return ok();
+}
+
 }  // extern "C"
 
 namespace {

@@ -62,6 +62,7 @@
 
 #include "gdr_device.hpp"
 #include "gdr_internal.hpp"
+#include "gdr_staged.hpp"
 
 namespace rhz {
 
@@ -95,7 +96,7 @@ struct ChunkParams {
 // The fused-prologue instances' launch and device counters (compiled in
 // gdr_chunked_pre.hip).
 hipError_t chunked_go_prologue(const ChunkParams& cp, int dk, int blocks, hipStream_t st);
-// which: 0 = LDS waits that gave up, 1 = fp16 range errors.
+// which: 0 = LDS waits that gave up, 1 = fp16 range errors, 2 = exact reruns.
 hipError_t chunked_prologue_counter(int which, unsigned int* count, bool reset);
 
 namespace {
@@ -105,10 +106,18 @@ namespace {
 __device__ unsigned int g_sync_timeouts;
 // Number of (workgroup, wave) pairs since the last reset in which an fp16
 // entry of A or P (the MFMA operands formed from q and k) was NaN,
-// infinite or too large for fp16 (|x| >= 65520): q or k elements or their
-// inner products beyond fp16's range, or non-finite q or k.  The operands
-// formed from v and the state are rescaled by powers of two instead.
+// infinite or too large for fp16 (|x| >= 65520) and the workgroup's results
+// were not recomputed: only the fused-prologue instances count here (their
+// q and k rows are normalised in the kernel); the plain instances rerun
+// such a tile exactly instead.  The operands formed from v and the state are
+// rescaled by powers of two.
 __device__ unsigned int g_range_errors;
+// Number of workgroups since the last reset that recomputed their rows with
+// the fp32 recurrence (staged_rows) because an input left the domain in
+// which the fp16 operands are accurate: an entry of A or P out of fp16's
+// range or not finite, a key row with |k|^2 > kKeyNormSqMax, a beta outside
+// [0, 1], or a decay alpha outside [0, 1] (log-decay above 0 or NaN).
+__device__ unsigned int g_exact_reruns;
 
 constexpr int kTV = 32;           // rows of S per workgroup (two scan waves of 16)
 constexpr int kMaxSortSeqs = 4096;
@@ -118,6 +127,11 @@ constexpr int kLDT = 64;          // fp16 row stride of the 64x64 tiles A, T, P
 constexpr int kLDV = 68;          // fp32 row stride of the beta V tile
 constexpr int kLDD = 20;          // fp32 row stride of A's diagonal blocks
 constexpr int kGateWave = 3;      // loader wave (of 4) that processes the gates
+// Largest |k|^2 of the chunked path's domain: unit rows (delta.rs:17-20)
+// after bf16 rounding (|k|^2 <= (1 + 2^-9)^2), with margin.  Within it, and
+// with beta and alpha in [0, 1], |A_rs| <= |k_r||k_s| stays near 1 and T
+// stays well inside fp16's range.
+constexpr float kKeyNormSqMax = 1.03125f;
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -259,16 +273,6 @@ __device__ __forceinline__ int tok(int b, int m) { return 32 * (b >> 1) + 8 * (m
 
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ void seq_bounds(const int* cu, int seq, int seq_len, int& t0, int& t1) {
-    if (cu) {
-        t0 = min(max(cu[seq], 0), seq_len);
-        t1 = min(max(cu[seq + 1], t0), seq_len);
-    } else {
-        t0 = seq * seq_len;
-        t1 = t0 + seq_len;
-    }
-}
-
 // Inclusive prefix sum over the 64 lanes of a wave: shifts within rows of
 // 16 lanes, then row 0's total into row 1 and row 2's into row 3
 // (row_bcast:15), then rows 0-1's total into rows 2-3 (row_bcast:31).
@@ -386,6 +390,14 @@ struct Sync {
     int tfull;   // waves 2, 3 (2 per chunk): T complete
     int pdone;   // loader waves (4 per chunk): P
     int scanned[2];  // scan wave w (1 per chunk): its last read of the chunk's buffers returned
+    int rerun;       // nonzero: an input left the fp16 path's domain (set once, read after the loops)
+};
+
+// What the exact rerun needs, written by one thread before the chunk loops
+// and read after them, so that no register holds it through the loops.
+struct RerunArgs {
+    SeqParams sp;
+    int seq, h, i0;
 };
 constexpr int kSpinLimit = 1 << 20;
 
@@ -437,10 +449,13 @@ __device__ __forceinline__ void range_watch(uint32_t& rng, uint2 h) {
     rng = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, rng),
                                                                  __builtin_elementwise_max(a, b)));
 }
+// Whether this lane's watch saw such a value.
+__device__ __forceinline__ bool range_bad(uint32_t rng) {
+    return (rng & 0xffffu) >= 0x7c00u || (rng >> 16) >= 0x7c00u;
+}
 // One count in g_range_errors when any lane of the wave saw such a value.
-__device__ __forceinline__ void note_range(uint32_t rng) {
-    const bool bad = (rng & 0xffffu) >= 0x7c00u || (rng >> 16) >= 0x7c00u;
-    if (__builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicAdd(&g_range_errors, 1u);
+[[maybe_unused]] __device__ __forceinline__ void note_range(uint32_t rng) {
+    if (__builtin_amdgcn_ballot_w64(range_bad(rng)) != 0 && (threadIdx.x & 63) == 0) atomicAdd(&g_range_errors, 1u);
 }
 
 // Shared memory of one workgroup.  Buffers indexed [2] are double-buffered
@@ -466,7 +481,17 @@ struct Smem {
     float seg[2][64];                // segment of token s: resets at or before s
     int resets[2];                   // the chunk has a reset (seg is then valid)
     Sync sync;
+    RerunArgs rerun_args;
 };
+
+// Marks the workgroup for the exact rerun when any lane of the wave saw an
+// input outside the fp16 path's domain; the flag is read once every role
+// has left its chunk loop.
+template <int DK>
+__device__ __forceinline__ void flag_rerun(Smem<DK>& sm, bool bad) {
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0)
+        __hip_atomic_store(&sm.sync.rerun, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 // Per-workgroup constants shared by the roles.
 struct Unit {
@@ -598,13 +623,25 @@ __device__ __forceinline__ void stage_gates_as(Smem<DK>& sm, int s, float g, flo
 }
 // PRE: the gate and beta loaded are logits, mapped as the prologue does
 // (g = -softplus(a_h) softplus(alpha_logit), beta = sigmoid(beta_logit)).
+// The plain gates' domain (beta and alpha in [0, 1]), tracked across
+// chunks: gmax is the running maximum of g + 1/2 and |beta - 1/2|, at most
+// 1/2 inside it; nan is set by a NaN gate or beta.
+struct GateDomain {
+    float gmax = 0.f;
+    int nan = 0;
+    __device__ __forceinline__ bool bad() const { return nan != 0 || !(gmax <= 0.5f); }
+};
 template <int DK, int NB, bool PRE>
 __device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int s, int len,
-                                            const ChunkIn<DK>& r) {
+                                            const ChunkIn<DK>& r, GateDomain& dom) {
     const float graw = PRE ? -u.spa * fast_softplus(r.g) : log_decay(r.g, p.gate_is_alpha);
     const bool rst = s < len && is_reset(graw);
     const float g = s < len && !rst ? graw : 0.f;
     const float beta = s < len ? (PRE ? fast_sigmoid(r.b) : r.b) : 0.f;
+    if constexpr (!PRE) {
+        dom.gmax = max3_abs3(dom.gmax, graw + 0.5f, beta - 0.5f);
+        dom.nan |= __builtin_isunordered(graw, beta) ? 1 : 0;
+    }
     if (__builtin_amdgcn_ballot_w64(rst) == 0)
         stage_gates_as<DK, NB, false>(sm, s, g, beta, rst);
     else
@@ -623,7 +660,7 @@ __device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, 
 // wave, so its squared norm is a sum over those lanes.
 template <int DK, int NB, bool GATES, bool PRE>
 __device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, const Unit& un, int len, int i0,
-                                            int lt, const ChunkIn<DK>& r) {
+                                            int lt, const ChunkIn<DK>& r, GateDomain& dom) {
     constexpr int PPR = DK / 8;
     if constexpr (PRE) {
         const uint4 z = make_uint4(0, 0, 0, 0);
@@ -647,7 +684,7 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, 
             sm.vb[NB][(c8 + 2 * e) * kLDV + row] = ok ? bv * __uint_as_float(wv[e] << 16) : 0.f;
             sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = ok ? bv * __uint_as_float(wv[e] & 0xffff0000u) : 0.f;
         }
-        if constexpr (GATES) stage_gates<DK, NB, true>(p, sm, un, lt & 63, len, r);
+        if constexpr (GATES) stage_gates<DK, NB, true>(p, sm, un, lt & 63, len, r, dom);
         return;
     }
     const bool full = len == kChunk && p.d_k == DK && i0 + kTV <= p.d_v;  // uniform
@@ -696,7 +733,7 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, Smem<DK>& sm, 
             sm.vb[NB][(c8 + 2 * e + 1) * kLDV + row] = ok ? r.bv * __uint_as_float(wv[e] & 0xffff0000u) : 0.f;
         }
     }
-    if constexpr (GATES) stage_gates<DK, NB, false>(p, sm, un, lt & 63, len, r);
+    if constexpr (GATES) stage_gates<DK, NB, false>(p, sm, un, lt & 63, len, r, dom);
 }
 
 // ------------------------------------------------------------ K K^T, Q K^T
@@ -720,9 +757,12 @@ __device__ __forceinline__ void load_rows(const uint16_t* src, int blk, int n, i
 // product of three factors <= 1, exp(G_r - G_{16 BI}) exp(G_{16 BI} -
 // G_{16 BJ + 15}) exp(G_{16 BJ + 15} - G_s).  Diagonal blocks are masked to
 // s < r (A, kept in fp32 for the substitution) or s <= r (P).  The fp16
-// values pass through rng's range watch.
+// values pass through rng's range watch.  kmax keeps the running maximum of
+// the unmasked products of A's diagonal blocks: it bounds max_r |k_r|^2 from
+// below by the diagonal entries and is bounded by it (|k_r.k_s| <= |k_r||k_s|).
 template <int DK, int NB, bool ISQ, int BI, int BJ>
-__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l, uint32_t& rng) {
+__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l, uint32_t& rng,
+                                         float& kmax) {
     constexpr int NK = DK / 32;
     constexpr bool diag = BI == BJ;
     const int n = l & 15, g = l >> 4;
@@ -746,6 +786,7 @@ __device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f1
         range_watch(rng, h);
         *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = h;
     } else {
+        if constexpr (!ISQ) kmax = max3_raw(max3_raw(kmax, acc[0], acc[1]), acc[2], acc[3]);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int s = s0 + v;
@@ -870,7 +911,7 @@ __device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
 // Wave 2, chunk x (buffer B = x & 1): K K^T's diagonal blocks and T's
 // diagonal blocks, then T_10, T_20, T_30.
 template <int DK, int B>
-__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim) {
+__device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim, float& kmax) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     // K[B] staged; T[B] was read by the scan and written by both waves for chunk x - 2
@@ -880,10 +921,10 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim) 
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
     uint32_t unused = 0;  // diagonal blocks of A stay fp32
-    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l, unused);
-    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l, unused);
-    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l, unused);
-    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l, unused);
+    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l, unused, kmax);
+    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l, unused, kmax);
+    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l, unused, kmax);
+    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l, unused, kmax);
     lds_fence();
     t_diag<DK, B>(sm, l);
     signal(&sm.sync.tdiag);
@@ -903,15 +944,16 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
     const int n = l & 15, g = l >> 4;
     // K[B] staged; A (one buffer) was read by T's blocks of chunk x - 1
     wait_all<2>(lim, {&sm.sync.staged, &sm.sync.tfull}, {4 * (x + 1), 2 * x});
+    float unused = 0.f;  // off-diagonal blocks: no norm bound
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
-    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l, rng);
-    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l, rng);
-    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l, rng);
-    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l, rng);
-    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l, rng);
-    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l, rng);
+    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l, rng, unused);
+    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l, rng, unused);
+    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l, rng, unused);
+    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l, rng, unused);
+    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l, rng, unused);
+    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l, rng, unused);
     signal(&sm.sync.aoff);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
@@ -927,35 +969,36 @@ template <int DK, int NB, int LW>
 __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
+    float unused = 0.f;  // Q K^T: no norm bound
     f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
     if constexpr (LW == 0) {
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 0, n, g, y0);
         load_rows<DK>(sm.q[NB], 1, n, g, y1);
-        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l, rng);
-        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l, rng);
+        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l, rng, unused);
+        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l, rng, unused);
     } else if constexpr (LW == 1) {
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.q[NB], 1, n, g, y0);
         load_rows<DK>(sm.q[NB], 2, n, g, y1);
-        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l, rng);
-        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l, rng);
+        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l, rng, unused);
+        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l, rng, unused);
     } else if constexpr (LW == 2) {
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 2, n, g, y0);
         load_rows<DK>(sm.q[NB], 3, n, g, y1);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l, rng);
-        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l, rng);
-        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l, rng);
+        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l, rng, unused);
+        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l, rng, unused);
+        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l, rng, unused);
     } else {
         load_rows<DK>(sm.q[NB], 3, n, g, y0);
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l, rng);
-        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l, rng);
+        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l, rng, unused);
+        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l, rng, unused);
         load_rows<DK>(sm.k[NB], 3, n, g, x0);
-        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l, rng);
+        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l, rng, unused);
     }
 }
 
@@ -965,13 +1008,13 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
 template <int DK, int B, int LW, bool PRE>
 __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, const Unit& u, int x, int lt,
                                             const LoadOffsets<DK>& lo, const LoadOffsets<DK>& lastc,
-                                            ChunkIn<DK>& in, uint32_t& rng) {
+                                            ChunkIn<DK>& in, uint32_t& rng, GateDomain& dom) {
     // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
     Sync& sy = sm.sync;
     wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
                 {x - 1, x - 1, 4 * (x - 1), x - 1, x - 1});
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
-    stage_chunk<DK, B, LW == kGateWave, PRE>(p, sm, u, len, u.i0, lt, in);
+    stage_chunk<DK, B, LW == kGateWave, PRE>(p, sm, u, len, u.i0, lt, in, dom);
     signal(&sm.sync.staged);
     load_chunk_any<DK>(p, u, x + 2, lo, lastc, in);
     wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
@@ -989,12 +1032,16 @@ __device__ __forceinline__ void loader_loop(const ChunkParams& p, Smem<DK>& sm, 
     load_chunk_any<DK>(p, u, 0, lo, lastc, in0);
     load_chunk_any<DK>(p, u, 1, lo, lastc, in1);
     uint32_t rng = 0;
+    GateDomain dom;
     for (int x = 0; x < u.nch; x += 2) {
-        prep_loader<DK, 0, LW, PRE>(p, sm, u, x, lt, lo, lastc, in0, rng);
+        prep_loader<DK, 0, LW, PRE>(p, sm, u, x, lt, lo, lastc, in0, rng, dom);
         if (x + 1 >= u.nch) break;
-        prep_loader<DK, 1, LW, PRE>(p, sm, u, x + 1, lt, lo, lastc, in1, rng);
+        prep_loader<DK, 1, LW, PRE>(p, sm, u, x + 1, lt, lo, lastc, in1, rng, dom);
     }
-    note_range(rng);
+    if constexpr (PRE)
+        note_range(rng);
+    else
+        flag_rerun(sm, range_bad(rng) || (LW == kGateWave && dom.bad()));
 }
 
 // ------------------------------------------------------------ scan waves
@@ -1222,15 +1269,20 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
 }
 
 // ------------------------------------------------------------ fused kernel
-// PRE: the fused prologue (raw q, k projections and gate / beta logits).
-template <int DK, bool PRE>
-__global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
-    constexpr int NK = DK / 32;
-    __shared__ __align__(16) Smem<DK> sm;
+// Shared memory of the chunk loops, reused by the exact rerun.
+template <int DK>
+union KernelSmem {
+    Smem<DK> chunk;
+    StageSmem<8> rerun;  // 16 * 8 = 128 key columns, 32 rows: one tile
+};
+static_assert(StageSmem<8>::RPB == kTV, "the exact rerun covers one tile of rows");
 
+// Workgroup bid -> its (sequence, head, rows) and token range.
+template <bool PRE>
+__device__ __forceinline__ Unit make_unit(const ChunkParams& p, int bid) {
     const int H = p.heads;
     int unit, tile;
-    map_block(blockIdx.x, p.batch * H, p.n_tiles, unit, tile);
+    map_block(bid, p.batch * H, p.n_tiles, unit, tile);
     const int seqi = unit / H;
     Unit u;
     u.h = unit - seqi * H;
@@ -1241,6 +1293,30 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     u.nch = (u.te - u.tb + kChunk - 1) / kChunk;
     u.i0 = tile * kTV;
     u.spa = PRE && u.nch > 0 ? softplus_f(p.a_log[u.h]) : 0.f;
+    return u;
+}
+
+// The exact rerun of a tile whose inputs left the fp16 path's domain: the
+// whole workgroup, once every role has left its chunk loop, recomputes the
+// tile's rows from the initial state with the fp32 recurrence, overwriting
+// the outputs and the final state the chunk loops wrote.  Its arguments
+// come from LDS (rerun_args), read before the rerun reuses that memory.
+template <int DK>
+__device__ __forceinline__ void exact_rerun(KernelSmem<DK>& smu) {
+    const RerunArgs ra = smu.chunk.rerun_args;
+    __syncthreads();  // every wave has read the flag and the arguments: the LDS is free
+    staged_rows<8, uint16_t>(ra.sp, smu.rerun, ra.seq, ra.h, ra.i0, threadIdx.x);
+}
+
+// PRE: the fused prologue (raw q, k projections and gate / beta logits).
+template <int DK, bool PRE>
+__global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
+    constexpr int NK = DK / 32;
+    __shared__ __align__(16) KernelSmem<DK> smu;
+    Smem<DK>& sm = smu.chunk;
+
+    const int H = p.heads;
+    const Unit u = make_unit<PRE>(p, blockIdx.x);
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int dk = p.d_k, dv = p.d_v;
@@ -1250,7 +1326,13 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         uint4* base = reinterpret_cast<uint4*>(it < 2 * 64 * kLDT / 8 ? &sm.t[0][0] : &sm.p[0][0]);
         base[it % (2 * 64 * kLDT / 8)] = make_uint4(0, 0, 0, 0);
     }
-    if (tid == 0) sm.sync = Sync{0, 0, 0, 0, 0, {0, 0}};
+    if (tid == 0) {
+        sm.sync = Sync{0, 0, 0, 0, 0, {0, 0}, 0};
+        if constexpr (!PRE)
+            sm.rerun_args = RerunArgs{{p.q, p.k, p.v, p.gate, p.beta, p.cu_seqlens, p.init, p.fin, p.o, p.seq_len,
+                                       p.heads, p.d_k, p.d_v, p.gate_is_alpha},
+                                      u.seq, u.h, u.i0};
+    }
     __syncthreads();  // the only workgroup barrier: the chunk loops sync through sm.sync
 
     // Every role runs chunks 0 .. nch-1, unrolled by two so that buffer c & 1
@@ -1291,17 +1373,22 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
             }
         }
     } else if (w == 2) {
+        float kmax = 0.f;
         for (int x = 0; x < u.nch; x += 2) {
-            prep_wave2<DK, 0>(sm, x, l, p.spin_limit);
-            if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l, p.spin_limit);
+            prep_wave2<DK, 0>(sm, x, l, p.spin_limit, kmax);
+            if (x + 1 < u.nch) prep_wave2<DK, 1>(sm, x + 1, l, p.spin_limit, kmax);
         }
+        if constexpr (!PRE) flag_rerun(sm, !(kmax <= kKeyNormSqMax));
     } else if (w == 3) {
         uint32_t rng = 0;
         for (int x = 0; x < u.nch; x += 2) {
             prep_wave3<DK, 0>(sm, x, l, p.spin_limit, rng);
             if (x + 1 < u.nch) prep_wave3<DK, 1>(sm, x + 1, l, p.spin_limit, rng);
         }
-        note_range(rng);
+        if constexpr (PRE)
+            note_range(rng);
+        else
+            flag_rerun(sm, range_bad(rng));
     } else if (w == 4) {
         loader_loop<DK, 0, PRE>(p, sm, u, tid - 256);
     } else if (w == 5) {
@@ -1311,19 +1398,29 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
     } else {
         loader_loop<DK, 3, PRE>(p, sm, u, tid - 256);
     }
+
+    if constexpr (!PRE) {
+        __syncthreads();  // every role has left its loop and set its flag
+        const int rerun = __hip_atomic_load(&sm.sync.rerun, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (rerun != 0) {  // uniform over the workgroup
+            if (threadIdx.x == 0) atomicAdd(&g_exact_reruns, 1u);
+            exact_rerun<DK>(smu);
+        }
+    }
 }
 
 // The value a counter held when read_counter swapped it (one per device and
 // compilation unit).
 __device__ unsigned int g_counter_read;
 
-// Reads counter `which` (0: g_sync_timeouts, 1: g_range_errors) into
+// Reads counter `which` (0: g_sync_timeouts, 1: g_range_errors, 2:
+// g_exact_reruns) into
 // g_counter_read and, when reset is set, zeroes it in the same atomic
 // exchange, so that a count added by a kernel still running elsewhere on the
 // device lands either in this read or in the next one, never in neither.
 __global__ __launch_bounds__(64) void gdr_counter_swap_kernel(int which, int reset) {
     if (threadIdx.x != 0) return;
-    unsigned int* c = which == 0 ? &g_sync_timeouts : &g_range_errors;
+    unsigned int* c = which == 0 ? &g_sync_timeouts : which == 1 ? &g_range_errors : &g_exact_reruns;
     g_counter_read = reset ? atomicExch(c, 0u) : __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1389,6 +1486,9 @@ hipError_t chunked_range_errors(unsigned int* count, bool reset) {
     *count = a + b;
     return e;
 }
+
+// Only the plain instances rerun tiles.
+hipError_t chunked_exact_reruns(unsigned int* count, bool reset) { return read_counter(2, count, reset); }
 
 namespace {
 

@@ -45,9 +45,13 @@ hipError_t launch_chunked_noalloc(const rhz_gdr_prefill_args& a, hipStream_t str
 // Reads (and with `reset`, zeroes) the current device's count of chunked-kernel
 // LDS waits that gave up.  Synchronous with respect to the device.
 hipError_t chunked_sync_timeouts(unsigned int* count, bool reset);
-// The same for the count of chunked-kernel steps whose fp16 operands were not
-// finite or beyond fp16's range.
+// The same for the count of (workgroup, wave) pairs of the fused-prologue
+// instances that saw an fp16 operand that was not finite or beyond fp16's
+// range.
 hipError_t chunked_range_errors(unsigned int* count, bool reset);
+// The same for the count of workgroups that recomputed their rows with the
+// fp32 recurrence because an input left the fp16 path's domain.
+hipError_t chunked_exact_reruns(unsigned int* count, bool reset);
 
 // Local-block prologue and epilogue (gdr_aux.hip).
 hipError_t launch_conv1d(const rhz_conv1d_args& a, hipStream_t stream);

@@ -15,19 +15,15 @@
 //                         the positions staged through LDS in blocks (d_k <=
 //                         128) or loaded one position ahead (any shape).
 //
-// Rows of S are independent (row i only reads v_i and its own row), so
-// both kernels give each row to a group of LPR = d_k_max / 16 lanes; lane li
-// of a group holds columns c*4*LPR + 4*li + e (c, e in 0..3), so every
-// 16-byte load of a wave covers whole contiguous row segments.  Per row and
-// token the two dot products S_i.k and S_i.q and the shared k.q are summed
-// over the group with a fixed butterfly, then
+// The per-row update and its lane layout are those of gdr_staged.hpp: each
+// row of S goes to a group of LPR lanes, and per row and token
 //     c_i  = beta * (v_i - alpha * (S_i.k))
 //     o_i  = alpha * (S_i.q) + c_i * (k.q)        (= S_i' . q)
 //     S_i' = alpha * S_i + c_i * k                (one FMA per element)
-// so the state is read once and written once per position.
 
 #include "gdr_device.hpp"
 #include "gdr_internal.hpp"
+#include "gdr_staged.hpp"
 
 namespace rhz {
 namespace {
@@ -55,38 +51,6 @@ struct MultiParams {
     int steps, heads, d_k, d_v, gate_is_alpha;
 };
 
-struct SeqParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    const float* gate;
-    const float* beta;
-    const int* cu_seqlens;
-    const float* init;
-    float* fin;
-    void* o;
-    int seq_len, heads, d_k, d_v, gate_is_alpha;
-};
-
-// The 16 columns of a row held by lane li of its group (zero outside [0, n)).
-template <int LPR, bool VEC, typename T>
-__device__ __forceinline__ void load_slice(const T* row, int li, int n, float (&x)[16]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int col = c * 4 * LPR + 4 * li;
-        if (VEC) {
-            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (col < n) f = load4(row + col);
-            x[4 * c + 0] = f.x;
-            x[4 * c + 1] = f.y;
-            x[4 * c + 2] = f.z;
-            x[4 * c + 3] = f.w;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[4 * c + e] = (col + e < n) ? Elem<T>::load(row, col + e) : 0.f;
-        }
-    }
-}
 
 // The same rows by non-temporal loads (a state streamed through once).
 template <int LPR>
@@ -100,54 +64,6 @@ __device__ __forceinline__ void load_slice_nt(const float* row, int li, int n, f
         x[4 * c + 1] = f[1];
         x[4 * c + 2] = f[2];
         x[4 * c + 3] = f[3];
-    }
-}
-
-// NT: non-temporal stores (streaming output that this kernel does not read
-// back, such as the multistep snapshots).
-template <int LPR, bool VEC, bool NT = false>
-__device__ __forceinline__ void store_slice(float* row, int li, int n, const float (&x)[16]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int col = c * 4 * LPR + 4 * li;
-        if (VEC) {
-            if (col < n) {
-                if (NT) {
-                    const f32x4 val = {x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
-                    __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(row + col));
-                } else {
-                    *reinterpret_cast<float4*>(row + col) =
-                        make_float4(x[4 * c + 0], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < n) row[col + e] = x[4 * c + e];
-        }
-    }
-}
-
-__device__ __forceinline__ float dot16(const float (&a)[16], const float (&b)[16]) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        s0 += a[4 * c + 0] * b[4 * c + 0];
-        s1 += a[4 * c + 1] * b[4 * c + 1];
-        s2 += a[4 * c + 2] * b[4 * c + 2];
-        s3 += a[4 * c + 3] * b[4 * c + 3];
-    }
-    return (s0 + s1) + (s2 + s3);
-}
-
-// Sequence bounds of packed sequence `seq`, clamped into [0, total].
-__device__ __forceinline__ void seq_bounds(const int* cu, int seq, int seq_len, int& t0, int& t1) {
-    if (cu) {
-        t0 = min(max(cu[seq], 0), seq_len);
-        t1 = min(max(cu[seq + 1], t0), seq_len);
-    } else {
-        t0 = seq * seq_len;
-        t1 = t0 + seq_len;
     }
 }
 
@@ -353,167 +269,16 @@ __global__ __launch_bounds__(64) void gdr_recurrent_kernel(SeqParams p) {
 
 // ------------------------------------------------ staged recurrent prefill
 // The same recurrence with the positions staged through LDS in blocks of
-// kStageTokens, for d_k <= 128 (LPR = 2, 4 or 8).  One workgroup of four
-// waves per (sequence, head, 4 * 64 / LPR rows): every thread loads its
-// share of block b + 1 -- k and q rows of the head, the workgroup's v rows,
-// the gates -- into registers while the waves run block b from LDS, then
-// writes it to the other LDS buffer together with k.q of each position
-// (summed once per workgroup instead of once per row).  A wave then reads
-// each position's k and q from LDS, sums S_i.k and S_i.q over its row's
-// lanes by DPP, and updates its rows as gdr_recurrent_kernel does.  The
-// global loads of a block have a whole block's compute to arrive.
-constexpr int kStageTokens = 32;
-constexpr int kStageWaves = 4;
-
-template <int LPR>
-struct StageSmem {
-    static constexpr int DKP = 16 * LPR;                    // padded key width
-    static constexpr int RPB = kStageWaves * (64 / LPR);    // state rows per workgroup
-    float k[2][kStageTokens][DKP];
-    float q[2][kStageTokens][DKP];
-    float v[2][kStageTokens][RPB];
-    float4 gb[2][kStageTokens];  // (alpha, beta, k.q, 0)
-};
-
-// One block's inputs in registers between their global load and their LDS
-// write.  Piece m of thread j is float4 number f = j + 256 m of the block's
-// row-major [token][DKP] k (and q) tile; v likewise over [token][RPB].
-template <int LPR>
-struct StageRegs {
-    static constexpr int NKQ = kStageTokens * (16 * LPR) / 4 / 256;
-    static constexpr int NV = kStageTokens * (kStageWaves * (64 / LPR)) / 4 / 256;
-    float4 k[NKQ], q[NKQ], v[NV];
-    float g, b;
-};
-
+// kStageTokens, for d_k <= 128 (LPR = 2, 4 or 8): one workgroup of four
+// waves per (sequence, head, 4 * 64 / LPR rows), running staged_rows
+// (gdr_staged.hpp).  The global loads of a block have a whole block's
+// compute to arrive.
 template <int LPR, typename T>
-__device__ __forceinline__ void stage_load(const SeqParams& p, int h, int i0, int tb, int len, int j,
-                                           StageRegs<LPR>& r) {
-    constexpr int DKP = 16 * LPR, RPB = kStageWaves * (64 / LPR);
-    const long H = p.heads;
-    const T* kp = static_cast<const T*>(p.k);
-    const T* qp = static_cast<const T*>(p.q);
-    const T* vp = static_cast<const T*>(p.v);
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NKQ; ++m) {
-        const int f = j + 256 * m, tt = f / (DKP / 4), col = 4 * (f % (DKP / 4));
-        const bool ok = tt < len && col < p.d_k;
-        const long off = ((long)(tb + tt) * H + h) * p.d_k + col;
-        r.k[m] = ok ? load4(kp + off) : z;
-        r.q[m] = ok ? load4(qp + off) : z;
-    }
-#pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NV; ++m) {
-        const int f = j + 256 * m, tt = f / (RPB / 4), rr = 4 * (f % (RPB / 4));
-        const bool ok = tt < len && i0 + rr < p.d_v;
-        r.v[m] = ok ? load4(vp + ((long)(tb + tt) * H + h) * p.d_v + i0 + rr) : z;
-    }
-    const int tt = j & (kStageTokens - 1);
-    const bool ok = j < 2 * kStageTokens && tt < len;
-    const float x = ok ? (j < kStageTokens ? p.gate : p.beta)[(long)(tb + tt) * H + h] : 0.f;
-    r.g = x;  // lanes 0..31: gates, 32..63: betas (consumed by wave 0)
-    r.b = x;
-}
-
-// Writes a block from registers to LDS buffer B, with alpha, beta and k.q of
-// every position.  Positions past the sequence's end hold zeros.
-template <int LPR>
-__device__ __forceinline__ void stage_store(const SeqParams& p, StageSmem<LPR>& sm, int B, int j,
-                                            const StageRegs<LPR>& r) {
-    constexpr int DKP = 16 * LPR, RPB = kStageWaves * (64 / LPR);
-    constexpr int PPT = DKP / 4;  // float4 pieces per position: a group of PPT consecutive threads
-#pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NKQ; ++m) {
-        const int f = j + 256 * m, tt = f / PPT, col = 4 * (f % PPT);
-        *reinterpret_cast<float4*>(&sm.k[B][tt][col]) = r.k[m];
-        *reinterpret_cast<float4*>(&sm.q[B][tt][col]) = r.q[m];
-        // k.q of position tt, summed over its PPT threads (PPT = 8, 16 or 32)
-        float d = r.k[m].x * r.q[m].x + r.k[m].y * r.q[m].y + r.k[m].z * r.q[m].z + r.k[m].w * r.q[m].w;
-        d = lane_group_sum<(PPT < 16 ? PPT : 16)>(d);
-        if constexpr (PPT == 32) d += __shfl_xor(d, 16, kWave);
-        if ((f % PPT) == 0) sm.gb[B][tt].z = d;
-    }
-#pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NV; ++m) {
-        const int f = j + 256 * m, tt = f / (RPB / 4), rr = 4 * (f % (RPB / 4));
-        *reinterpret_cast<float4*>(&sm.v[B][tt][rr]) = r.v[m];
-    }
-    if (j < kStageTokens) {
-        sm.gb[B][j].x = decay_factor(r.g, p.gate_is_alpha);
-        sm.gb[B][j].w = 0.f;
-    } else if (j < 2 * kStageTokens) {
-        sm.gb[B][j - kStageTokens].y = r.b;
-    }
-}
-
-template <int LPR, typename T>
-__global__ __launch_bounds__(256) void gdr_staged_recurrent_kernel(SeqParams p) {
-    constexpr int RPW = 64 / LPR, RPB = kStageWaves * RPW;
+__global__ __launch_bounds__(kStageThreads) void gdr_staged_recurrent_kernel(SeqParams p) {
     __shared__ __align__(16) StageSmem<LPR> sm;
     const int unit = blockIdx.x;
     const int seq = unit / p.heads, h = unit % p.heads;
-    const int j = threadIdx.x, lane = j & 63, w = j >> 6;
-    const int li = lane % LPR;
-    const int rr = w * RPW + lane / LPR;  // row within the workgroup
-    const int i0 = blockIdx.y * RPB;
-    const int r = i0 + rr;
-    const int dk = p.d_k, dv = p.d_v, H = p.heads;
-    const bool row_ok = r < dv;
-    int t0, t1;
-    seq_bounds(p.cu_seqlens, seq, p.seq_len, t0, t1);
-    const int nb = (t1 - t0 + kStageTokens - 1) / kStageTokens;
-
-    float s[16];
-    if (p.init && row_ok) {
-        load_slice<LPR, true, float>(p.init + ((long)unit * dv + r) * dk, li, dk, s);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = 0.f;
-    }
-    T* op = static_cast<T*>(p.o);
-
-    StageRegs<LPR> regs;
-    if (nb > 0) {
-        stage_load<LPR, T>(p, h, i0, t0, min(kStageTokens, t1 - t0), j, regs);
-        stage_store<LPR>(p, sm, 0, j, regs);
-    }
-    __syncthreads();
-    T* orow = op + (long)h * dv + r;  // o of position t at orow + t * H * dv
-    const long ostride = (long)H * dv;
-    for (int b = 0; b < nb; ++b) {
-        const int B = b & 1;
-        const int tb = t0 + b * kStageTokens;
-        const int len = min(kStageTokens, t1 - tb);
-        const bool more = b + 1 < nb;  // uniform
-        if (more) stage_load<LPR, T>(p, h, i0, tb + kStageTokens, min(kStageTokens, t1 - tb - kStageTokens), j, regs);
-        for (int tt = 0; tt < len; ++tt) {
-            float kr[16], qr[16];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float4 a = *reinterpret_cast<const float4*>(&sm.k[B][tt][c * 4 * LPR + 4 * li]);
-                const float4 e = *reinterpret_cast<const float4*>(&sm.q[B][tt][c * 4 * LPR + 4 * li]);
-                kr[4 * c] = a.x, kr[4 * c + 1] = a.y, kr[4 * c + 2] = a.z, kr[4 * c + 3] = a.w;
-                qr[4 * c] = e.x, qr[4 * c + 1] = e.y, qr[4 * c + 2] = e.z, qr[4 * c + 3] = e.w;
-            }
-            const float4 gb = sm.gb[B][tt];  // alpha, beta, k.q
-            const float vi = sm.v[B][tt][rr];
-            const float sk = lane_group_sum<LPR>(dot16(s, kr));
-            const float sq = lane_group_sum<LPR>(dot16(s, qr));
-            const float c = gb.y * fmaf(-gb.x, sk, vi);
-            const float oi = fmaf(gb.x, sq, c * gb.z);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = fmaf(gb.x, s[e], c * kr[e]);
-            if (li == 0 && row_ok) Elem<T>::store(orow, (long)(tb + tt) * ostride, oi);
-        }
-        if (more) {
-            // buffer B ^ 1 was last read in block b - 1, which every wave has
-            // left (the barrier below closed it)
-            stage_store<LPR>(p, sm, B ^ 1, j, regs);
-        }
-        __syncthreads();
-    }
-    if (p.fin && row_ok) store_slice<LPR, true>(p.fin + ((long)unit * dv + r) * dk, li, dk, s);
+    staged_rows<LPR, T>(p, sm, seq, h, blockIdx.y * StageSmem<LPR>::RPB, threadIdx.x);
 }
 
 int lanes_per_row(int d_k) { return d_k <= 32 ? 2 : d_k <= 64 ? 4 : d_k <= 128 ? 8 : 16; }
@@ -605,9 +370,9 @@ hipError_t staged_pick_lpr(const SeqParams& sp, int units, int dk, int dv, hipSt
     const int rpb = kStageWaves * (64 / lpr);
     dim3 grid(units, (dv + rpb - 1) / rpb);
     switch (lpr) {
-        case 2: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<2, T>), grid, dim3(256), 0, st, sp); break;
-        case 4: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<4, T>), grid, dim3(256), 0, st, sp); break;
-        default: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<8, T>), grid, dim3(256), 0, st, sp); break;
+        case 2: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<2, T>), grid, dim3(kStageThreads), 0, st, sp); break;
+        case 4: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<4, T>), grid, dim3(kStageThreads), 0, st, sp); break;
+        default: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<8, T>), grid, dim3(kStageThreads), 0, st, sp); break;
     }
     return hipGetLastError();
 }

@@ -166,15 +166,29 @@ def sync_timeouts(reset: bool = True) -> int:
 
 
 def fp16_range_errors(reset: bool = True) -> int:
-    """Number of (workgroup, wave) pairs, counted once per chunked launch,
-    on the current device since the last reset whose fp16 operands formed
-    from q and k were NaN, infinite or beyond fp16's range in any chunk (q,
-    k or their inner products too large, or non-finite q or k); 0 unless a
-    chunked launch may have gone wrong.  Waits for all of the device's
-    outstanding work on every stream first; the read and the reset are one
-    atomic exchange on the device."""
+    """Number of (workgroup, wave) pairs of fused-prologue launches
+    (local_prefill), counted once per launch, on the current device since
+    the last reset whose fp16 operands formed from q and k were NaN,
+    infinite or beyond fp16's range in any chunk (non-finite projections);
+    0 unless such a launch may have gone wrong.  The plain chunked path
+    reruns those workgroups exactly instead (exact_reruns).  Waits for all
+    of the device's outstanding work on every stream first; the read and the
+    reset are one atomic exchange on the device."""
     n = c_uint32(0)
     _abi.check(_abi.lib().rhz_gdr_fp16_range_errors(byref(n), 1 if reset else 0))
+    return n.value
+
+
+def exact_reruns(reset: bool = True) -> int:
+    """Number of chunked-kernel workgroups (32 state rows of a (sequence,
+    head) each) on the current device since the last reset that recomputed
+    their rows with the fp32 recurrence because an input left the fp16
+    path's domain (a key row with |k|^2 > 1.03125, beta or alpha outside
+    [0, 1], an fp16 operand out of range).  Their results are correct; the
+    count says how often the slower path ran.  Same synchronisation as
+    fp16_range_errors."""
+    n = c_uint32(0)
+    _abi.check(_abi.lib().rhz_gdr_exact_reruns(byref(n), 1 if reset else 0))
     return n.value
 
 

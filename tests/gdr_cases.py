@@ -153,16 +153,21 @@ class Prefill:
             return t.reshape(self.batch, self.seq_len, *t.shape[1:])
         return t
 
-    def run(self, **kw):
+    def run(self, reruns: int = 0, **kw):
+        """Prefill through the C ABI; asserts that no LDS wait of the chunked
+        kernel gave up and that exactly `reruns` of its workgroups recomputed
+        their rows with the fp32 recurrence (0: every input in the fp16
+        path's domain).  The counters are reset by the reads."""
         import rhizome_amd
 
         o, fin = rhizome_amd.prefill(self.shaped(self.q), self.shaped(self.k), self.shaped(self.v),
                                      self.shaped(self.g), self.shaped(self.beta),
                                      cu_seqlens=self.cu_dev, initial_state=self.init, **kw)
         torch.cuda.synchronize()
-        # no LDS wait of the chunked kernel gave up (the count is reset by the read)
         assert rhizome_amd.sync_timeouts() == 0, "a chunked-kernel LDS wait gave up"
         assert rhizome_amd.fp16_range_errors() == 0, "a chunked-kernel fp16 operand out of range"
+        n = rhizome_amd.exact_reruns()
+        assert n == reruns, f"{n} chunked workgroups reran their rows exactly, expected {reruns}"
         return o.reshape(self.n_tok, self.heads, self.d_v), fin
 
     def oracle(self, seqs=None, heads=None):

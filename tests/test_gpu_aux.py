@@ -326,7 +326,7 @@ def test_local_chain_through_conv_prepare(device):
     n_tok = sum(lengths)
     y = rhizome_amd.rmsnorm_heads(o.view(n_tok * H, dv), s, 1e-6)
     torch.cuda.synchronize()
-    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0 and rhizome_amd.exact_reruns() == 0
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
     # each stage against the oracle on that stage's device input
     check_close(q.double().cpu().numpy(), rq, BF16_TOL, "chain conv prepare q")
@@ -417,7 +417,7 @@ def test_fused_prologues_take_large_projections(device, big):
                                                       cu_seqlens=cu_dev)
     o2, fin2 = rhizome_amd.prefill(qp, kp, vp, g, beta, cu_seqlens=cu_dev, algo="chunked")
     torch.cuda.synchronize()
-    assert rhizome_amd.fp16_range_errors() == 0 and rhizome_amd.sync_timeouts() == 0
+    assert rhizome_amd.fp16_range_errors() == 0 and rhizome_amd.sync_timeouts() == 0 and rhizome_amd.exact_reruns() == 0
     # stage by stage: the prepared q, k against the oracle's prepare, the
     # prefill against the oracle on those (bf16) values
     check_close(qp.double().cpu().numpy(), rq, BF16_TOL, f"conv prepare q, element {big:g}")

@@ -276,41 +276,96 @@ def test_tiny_qk_entries(device):
     _check(w, o, fin, BF16_TOL, tag="tiny q, k entries, chunked")
 
 
-def test_fp16_range_count(device):
-    """The chunked path's fp16 operands (q, k, and the q.k and k.k blocks)
-    against fp16's range, 65520.  q rows of norm 6e4 (so |q_r . k_s| <= 6e4)
-    stay inside: parity holds and nothing is counted.  One q element of 7e4,
-    or one infinite k element, is counted by rhz_gdr_fp16_range_errors; the
-    recurrent fp32 path takes the 7e4 input to the oracle's tolerance."""
-    import rhizome_amd
-
+def test_q_rows_near_fp16_range(device):
+    """q rows of norm 6e4 keep every fp16 operand of the chunked path in range
+    (|q_r . k_s| <= 6e4 < 65520): parity with the oracle, and no workgroup
+    reruns."""
     w = Prefill(batch=1, heads=2, seq_len=130, d_k=64, d_v=64, dtype=torch.bfloat16, device=device,
                 state_std=0.02)
     w.q = (w.q.double() * 6e4).to(torch.bfloat16)
     w.q64 = w.q.double().cpu().numpy()
     assert float(np.abs(w.q64).max()) < 65520.0
-    rhizome_amd.fp16_range_errors(reset=True)
-    o, fin = w.run(algo="chunked")  # asserts a zero count
+    o, fin = w.run(algo="chunked")  # asserts no rerun and no range error
     _check(w, o, fin, BF16_TOL, tag="q rows of norm 6e4, chunked")
 
-    def count(q, k):
-        rhizome_amd.prefill(w.shaped(q), w.shaped(k), w.shaped(w.v), w.shaped(w.g), w.shaped(w.beta),
-                            initial_state=w.init, algo="chunked")
-        torch.cuda.synchronize()
-        return rhizome_amd.fp16_range_errors(reset=True)
 
-    assert count(w.q, w.k) == 0
-    q_big = w.q.clone()
-    q_big[70, 1, 5] = 7e4
-    assert count(q_big, w.k) > 0, "a q element beyond fp16's range was not counted"
-    k_inf = w.k.clone()
-    k_inf[3, 0, 0] = float("inf")
-    assert count(w.q, k_inf) > 0, "an infinite k element was not counted"
-    assert rhizome_amd.fp16_range_errors() == 0
-    w.q = q_big
-    w.q64 = q_big.double().cpu().numpy()
-    o, fin = w.run(algo="recurrent")
-    _check(w, o, fin, BF16_TOL, tag="q element 7e4, recurrent")
+def _leave_domain(w, case, seq, head):
+    """Edits workload w (device tensors and their f64 copies) so that
+    sequence `seq`, head `head` leaves the chunked path's fp16 domain."""
+    t0, t1 = int(w.cu[seq]), int(w.cu[seq + 1])
+    n = t1 - t0
+    if case == "q element 7e4":  # beyond fp16's range on chip
+        w.q[t0 + n // 2, head, 5] = 7e4
+    elif case == "k element 1e5, its beta 1e-12":  # beyond fp16's range; beta keeps the recurrence tame
+        w.k[t0 + 3, head, 0] = 1e5
+        w.beta[t0 + 3, head] = 1e-12
+    elif case == "k rows of norm^2 1.2":
+        w.k[t0:t1, head] = (w.k[t0:t1, head].double() * 1.2 ** 0.5).to(w.k.dtype)
+    elif case == "beta 1.2":
+        w.beta[t0 + n // 3:t0 + n // 3 + 10, head] = 1.2
+    elif case == "beta -0.1":
+        w.beta[t0 + 5, head] = -0.1
+    elif case == "alpha 1.05":
+        w.g[t1 - 30:t1 - 26, head] = float(np.log(1.05))
+    else:
+        raise ValueError(case)
+    w.q64, w.k64 = w.q.double().cpu().numpy(), w.k.double().cpu().numpy()
+    w.beta64, w.g64 = w.beta.double().cpu().numpy(), w.g.double().cpu().numpy()
+    w.alpha64 = np.exp(w.g64)
+
+
+OUT_OF_DOMAIN = ["q element 7e4", "k element 1e5, its beta 1e-12", "k rows of norm^2 1.2", "beta 1.2",
+                 "beta -0.1", "alpha 1.05"]
+
+
+@pytest.mark.parametrize("case", OUT_OF_DOMAIN)
+def test_out_of_domain_inputs_rerun_exactly(device, case):
+    """Inputs outside the domain in which the chunked path's fp16 operands
+    are accurate -- a q or k element beyond fp16's range, key rows of norm
+    above 1, a beta or alpha outside [0, 1] -- in one (sequence, head) of a
+    packed batch with initial states: exactly that unit's workgroups (3 row
+    tiles of d_v = 96) recompute their rows with the fp32 recurrence inside
+    the same launch, and every unit matches the oracle."""
+    w = Prefill(heads=2, d_k=128, d_v=96, lengths=[70, 0, 130, 1, 33], dtype=torch.bfloat16, device=device,
+                state_std=0.02)
+    _leave_domain(w, case, seq=2, head=1)
+    o, fin = w.run(algo="chunked", reruns=3)
+    _check(w, o, fin, BF16_TOL, tag=f"{case}, chunked with exact rerun")
+
+
+def test_out_of_domain_dense_every_unit(device):
+    """A dense batch in which every unit leaves the domain (q element 7e4 in
+    every (batch, head)): every workgroup reruns, and all match the oracle;
+    the same inputs in the domain rerun nothing."""
+    w = Prefill(batch=2, heads=3, seq_len=100, d_k=64, d_v=64, dtype=torch.bfloat16, device=device)
+    o, fin = w.run(algo="chunked")
+    _check(w, o, fin, BF16_TOL, tag="in domain")
+    for b in range(2):
+        for h in range(3):
+            w.q[b * 100 + 7 * h + 10, h, 3] = -7e4
+    w.q64 = w.q.double().cpu().numpy()
+    o, fin = w.run(algo="chunked", reruns=2 * 3 * 2)
+    _check(w, o, fin, BF16_TOL, tag="q elements -7e4 everywhere, chunked with exact rerun")
+
+
+def test_out_of_domain_alpha_given(device):
+    """Gates given as alpha (RHZ_GATE_ALPHA): a negative alpha and one above 1
+    take the exact rerun (their logarithm is NaN or positive) and match the
+    oracle."""
+    import rhizome_amd
+
+    w = Prefill(batch=1, heads=2, seq_len=150, d_k=64, d_v=32, dtype=torch.bfloat16, device=device,
+                state_std=0.02)
+    alpha = torch.exp(w.g)
+    alpha[20, 0] = -0.5
+    alpha[90, 1] = 1.02
+    w.alpha64 = alpha.double().cpu().numpy()
+    o, fin = rhizome_amd.prefill(w.shaped(w.q), w.shaped(w.k), w.shaped(w.v), alpha=w.shaped(alpha),
+                                 beta=w.shaped(w.beta), initial_state=w.init, algo="chunked")
+    torch.cuda.synchronize()
+    assert rhizome_amd.sync_timeouts() == 0 and rhizome_amd.fp16_range_errors() == 0
+    assert rhizome_amd.exact_reruns() == 2  # one row tile (d_v = 32) per head
+    _check(w, o.reshape(w.n_tok, w.heads, w.d_v), fin, BF16_TOL, tag="alpha -0.5 and 1.02, chunked")
 
 
 @pytest.mark.parametrize("algo,dtype,tol", PATHS)

@@ -31,8 +31,10 @@ def test_forced_giveups_are_counted(device):
     n = rhizome_amd.sync_timeouts(reset=True)
     print(f"forced give-ups counted: {n}", flush=True)
     assert n > 0
-    # waves that went on without their inputs may have met any values
+    # waves that went on without their inputs may have met any values (and
+    # so flagged their workgroups for the exact rerun)
     rhizome_amd.fp16_range_errors(reset=True)
+    rhizome_amd.exact_reruns(reset=True)
     # the count was reset; a normal launch counts none (checked inside run) and is right
     o2, fin2 = w.run(algo="chunked")
     ref_o, ref_f = w.oracle()

@@ -7,7 +7,8 @@ caller-provided workspace) bit for bit.  A dense batch and the fp32
 recurrent path, which use no scratch, must match too.  A call captured in a
 HIP graph must match on every replay, with eager noalloc calls that
 overwrite the scratch in between; a batch of more than 4096 sequences takes
-the identity-order path.  The size limit is checked before any HIP call.
+the identity-order path, and a unit outside the fp16 path's domain takes the
+exact rerun through either entry point.  The size limit is checked before any HIP call.
 """
 from ctypes import byref
 
@@ -111,6 +112,22 @@ def test_noalloc_dense_and_recurrent(device, algo, dtype):
     w = Prefill(batch=2, heads=2, seq_len=150, d_k=64, d_v=64, dtype=dtype, device=device, state_std=0.02)
     o1, f1 = _noalloc(w, algo)
     o2, f2 = w.run(algo=algo)
+    assert torch.equal(o1, o2) and torch.equal(f1, f2)
+
+
+@pytest.mark.gpu
+def test_noalloc_exact_rerun(device):
+    # a packed batch in which one (sequence, head) leaves the fp16 path's
+    # domain (key rows of norm^2 1.2): that unit's two row tiles rerun
+    # exactly through either entry point, with identical results
+    w = Prefill(heads=2, d_k=64, d_v=64, lengths=[40, 0, 150, 9], seed=3, dtype=torch.bfloat16,
+                device=device, state_std=0.02)
+    t0, t1 = int(w.cu[2]), int(w.cu[3])
+    w.k[t0:t1, 0] = (w.k[t0:t1, 0].double() * 1.2 ** 0.5).to(torch.bfloat16)
+    rhizome_amd.exact_reruns(reset=True)
+    o1, f1 = _noalloc(w, "chunked")
+    assert rhizome_amd.exact_reruns() == 2
+    o2, f2 = w.run(algo="chunked", reruns=2)
     assert torch.equal(o1, o2) and torch.equal(f1, f2)
 
 
