@@ -274,8 +274,9 @@ def prefill_leg(torch, steps, warmup, c, workload, profile_key) -> dict:
 def bench_prefill_fp32(torch, steps, warmup) -> dict:
     """The fp32-input path on the headline prefill shape: rhz_gdr_prefill with
     fp32 q/k/v/o and RHZ_ALGO_RECURRENT (gdr_staged_recurrent_kernel, token by
-    token, one wave per 8 state rows of a head, four waves sharing each
-    32-position block of k, q, gates and k.q staged through LDS)."""
+    token, one wave per 4 state rows of a head (16 lanes of 8 key columns per
+    row), eight waves sharing each 32-position block of k, q, gates and k.q
+    staged through LDS, two waves per SIMD)."""
     import rhizome_amd
     from rhizome_amd import _abi, gdr
 
@@ -319,10 +320,10 @@ def bench_prefill_fp32(torch, steps, warmup) -> dict:
             # one after the other, so the launch is bound by the per-position
             # latency of that chain, not by HBM
             "latency": {"ns_per_position": ms * 1e6 / T, "positions_per_wave": T,
-                        "waves": B * H * ((dv + 7) // 8)},
+                        "waves": B * H * ((dv + 3) // 4)},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "traffic": traffic_from_profiles("prefill_fp32"),
-                         "kernel": "gdr_staged_recurrent_kernel<8,float>", "algorithmic_bytes": nbytes,
+                         "kernel": "gdr_staged_recurrent_kernel<16,float,8,8>", "algorithmic_bytes": nbytes,
                          "launch_us": ms * 1e3,
                          "fp32_valu": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": PEAK_FP32_TFLOPS,
                                        "unit": "TFLOP/s",

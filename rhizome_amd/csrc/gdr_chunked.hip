@@ -271,7 +271,11 @@ __device__ __forceinline__ float fast_softplus(float x) { return x > 15.f ? x : 
 // lane group g (rows 4g..4g+3 of both blocks) holds 32c + 8g + 0..7.
 __device__ __forceinline__ int tok(int b, int m) { return 32 * (b >> 1) + 8 * (m >> 2) + 4 * (b & 1) + (m & 3); }
 
-__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Orders a wave's LDS writes before its own later LDS reads of the same
+// data.  The hardware performs one wave's LDS operations in order, so this
+// needs no wait, only that the compiler keeps the program order; making
+// writes visible to other waves is signal()'s job.
+__device__ __forceinline__ void lds_fence() { asm volatile("" ::: "memory"); }
 
 // Inclusive prefix sum over the 64 lanes of a wave: shifts within rows of
 // 16 lanes, then row 0's total into row 1 and row 2's into row 3

@@ -273,12 +273,12 @@ __global__ __launch_bounds__(64) void gdr_recurrent_kernel(SeqParams p) {
 // waves per (sequence, head, 4 * 64 / LPR rows), running staged_rows
 // (gdr_staged.hpp).  The global loads of a block have a whole block's
 // compute to arrive.
-template <int LPR, typename T>
-__global__ __launch_bounds__(kStageThreads) void gdr_staged_recurrent_kernel(SeqParams p) {
-    __shared__ __align__(16) StageSmem<LPR> sm;
+template <int LPR, typename T, int VPL, int NW>
+__global__ __launch_bounds__(NW * 64) void gdr_staged_recurrent_kernel(SeqParams p) {
+    __shared__ __align__(16) StageSmem<LPR, VPL, NW> sm;
     const int unit = blockIdx.x;
     const int seq = unit / p.heads, h = unit % p.heads;
-    staged_rows<LPR, T>(p, sm, seq, h, blockIdx.y * StageSmem<LPR>::RPB, threadIdx.x);
+    staged_rows<LPR, T, VPL, NW>(p, sm, seq, h, blockIdx.y * StageSmem<LPR, VPL, NW>::RPB, threadIdx.x);
 }
 
 int lanes_per_row(int d_k) { return d_k <= 32 ? 2 : d_k <= 64 ? 4 : d_k <= 128 ? 8 : 16; }
@@ -367,12 +367,20 @@ hipError_t recurrent_pick_lpr(const SeqParams& sp, int units, int dk, int dv, hi
 template <typename T>
 hipError_t staged_pick_lpr(const SeqParams& sp, int units, int dk, int dv, hipStream_t st) {
     const int lpr = lanes_per_row(dk);
+    if (lpr == 8) {
+        // d_k in (64, 128]: 16 lanes of 8 columns per row and eight waves of
+        // four rows, so that two waves share each SIMD and hide each
+        // other's latency along the position chain.
+        using Sh = StageShape<16, 8, 8>;
+        dim3 grid(units, (dv + Sh::RPB - 1) / Sh::RPB);
+        hipLaunchKernelGGL((gdr_staged_recurrent_kernel<16, T, 8, 8>), grid, dim3(Sh::THREADS), 0, st, sp);
+        return hipGetLastError();
+    }
     const int rpb = kStageWaves * (64 / lpr);
     dim3 grid(units, (dv + rpb - 1) / rpb);
     switch (lpr) {
-        case 2: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<2, T>), grid, dim3(kStageThreads), 0, st, sp); break;
-        case 4: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<4, T>), grid, dim3(kStageThreads), 0, st, sp); break;
-        default: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<8, T>), grid, dim3(kStageThreads), 0, st, sp); break;
+        case 2: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<2, T, 16, kStageWaves>), grid, dim3(kStageThreads), 0, st, sp); break;
+        default: hipLaunchKernelGGL((gdr_staged_recurrent_kernel<4, T, 16, kStageWaves>), grid, dim3(kStageThreads), 0, st, sp); break;
     }
     return hipGetLastError();
 }

@@ -89,16 +89,47 @@ __device__ __forceinline__ float dot16(const float (&a)[16], const float (&b)[16
     return (s0 + s1) + (s2 + s3);
 }
 
-// Positions per LDS block, and the waves that compute (four: 4 * 64 / LPR
-// state rows).
+// Positions per LDS block, and the default shape of the computing waves
+// (four: 4 * 64 / LPR state rows, 16 columns per lane).
 constexpr int kStageTokens = 32;
 constexpr int kStageWaves = 4;
 constexpr int kStageThreads = kStageWaves * kWave;
 
-template <int LPR>
+// The dot product of a lane's VPL columns (four partial sums).
+template <int VPL>
+__device__ __forceinline__ float dot_lane(const float (&a)[VPL], const float (&b)[VPL]) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int c = 0; c < VPL / 4; ++c) {
+        s0 += a[4 * c + 0] * b[4 * c + 0];
+        s1 += a[4 * c + 1] * b[4 * c + 1];
+        s2 += a[4 * c + 2] * b[4 * c + 2];
+        s3 += a[4 * c + 3] * b[4 * c + 3];
+    }
+    return (s0 + s1) + (s2 + s3);
+}
+
+// The staging layout of NW computing waves whose rows of S each go to LPR
+// lanes holding VPL columns: DKP key columns, RPB rows per workgroup.
+template <int LPR, int VPL = 16, int NW = kStageWaves>
+struct StageShape {
+    static constexpr int DKP = VPL * LPR;        // padded key width
+    static constexpr int RPW = 64 / LPR;         // rows per wave
+    static constexpr int RPB = NW * RPW;         // state rows per workgroup
+    static constexpr int THREADS = NW * kWave;
+    static constexpr int PPT = DKP / 4;          // float4 pieces of one position's k (or q)
+    static constexpr int KQ4 = kStageTokens * PPT;       // float4 pieces of a block's k (or q)
+    static constexpr int V4 = kStageTokens * RPB / 4;    // float4 pieces of a block's v
+    static constexpr int NKQ = (KQ4 + THREADS - 1) / THREADS;
+    static constexpr int NV = (V4 + THREADS - 1) / THREADS;
+    static_assert(VPL % 4 == 0 && VPL * LPR >= 4 && PPT <= 32, "supported staging shapes");
+};
+
+template <int LPR, int VPL = 16, int NW = kStageWaves>
 struct StageSmem {
-    static constexpr int DKP = 16 * LPR;                    // padded key width
-    static constexpr int RPB = kStageWaves * (64 / LPR);    // state rows per workgroup
+    using Shape = StageShape<LPR, VPL, NW>;
+    static constexpr int DKP = Shape::DKP;
+    static constexpr int RPB = Shape::RPB;
     float k[2][kStageTokens][DKP];
     float q[2][kStageTokens][DKP];
     float v[2][kStageTokens][RPB];
@@ -106,37 +137,37 @@ struct StageSmem {
 };
 
 // One block's inputs in registers between their global load and their LDS
-// write.  Piece m of thread j is float4 number f = j + 256 m of the block's
-// row-major [token][DKP] k (and q) tile; v likewise over [token][RPB].
-template <int LPR>
+// write.  Piece m of thread j is float4 number f = j + THREADS m of the
+// block's row-major [token][DKP] k (and q) tile; v likewise over
+// [token][RPB].
+template <int LPR, int VPL = 16, int NW = kStageWaves>
 struct StageRegs {
-    static constexpr int NKQ = kStageTokens * (16 * LPR) / 4 / kStageThreads;
-    static constexpr int NV = kStageTokens * (kStageWaves * (64 / LPR)) / 4 / kStageThreads;
-    float4 k[NKQ], q[NKQ], v[NV];
+    using Shape = StageShape<LPR, VPL, NW>;
+    float4 k[Shape::NKQ], q[Shape::NKQ], v[Shape::NV];
     float g, b;
 };
 
-template <int LPR, typename T>
+template <int LPR, int VPL, int NW, typename T>
 __device__ __forceinline__ void stage_load(const SeqParams& p, int h, int i0, int tb, int len, int j,
-                                           StageRegs<LPR>& r) {
-    constexpr int DKP = 16 * LPR, RPB = kStageWaves * (64 / LPR);
+                                           StageRegs<LPR, VPL, NW>& r) {
+    using S = StageShape<LPR, VPL, NW>;
     const long H = p.heads;
     const T* kp = static_cast<const T*>(p.k);
     const T* qp = static_cast<const T*>(p.q);
     const T* vp = static_cast<const T*>(p.v);
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NKQ; ++m) {
-        const int f = j + kStageThreads * m, tt = f / (DKP / 4), col = 4 * (f % (DKP / 4));
-        const bool ok = tt < len && col < p.d_k;
+    for (int m = 0; m < S::NKQ; ++m) {
+        const int f = j + S::THREADS * m, tt = f / S::PPT, col = 4 * (f % S::PPT);
+        const bool ok = f < S::KQ4 && tt < len && col < p.d_k;
         const long off = ((long)(tb + tt) * H + h) * p.d_k + col;
         r.k[m] = ok ? load4(kp + off) : z;
         r.q[m] = ok ? load4(qp + off) : z;
     }
 #pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NV; ++m) {
-        const int f = j + kStageThreads * m, tt = f / (RPB / 4), rr = 4 * (f % (RPB / 4));
-        const bool ok = tt < len && i0 + rr < p.d_v;
+    for (int m = 0; m < S::NV; ++m) {
+        const int f = j + S::THREADS * m, tt = f / (S::RPB / 4), rr = 4 * (f % (S::RPB / 4));
+        const bool ok = f < S::V4 && tt < len && i0 + rr < p.d_v;
         r.v[m] = ok ? load4(vp + ((long)(tb + tt) * H + h) * p.d_v + i0 + rr) : z;
     }
     const int tt = j & (kStageTokens - 1);
@@ -148,26 +179,28 @@ __device__ __forceinline__ void stage_load(const SeqParams& p, int h, int i0, in
 
 // Writes a block from registers to LDS buffer B, with alpha, beta and k.q of
 // every position.  Positions past the sequence's end hold zeros.
-template <int LPR>
-__device__ __forceinline__ void stage_store(const SeqParams& p, StageSmem<LPR>& sm, int B, int j,
-                                            const StageRegs<LPR>& r) {
-    constexpr int DKP = 16 * LPR, RPB = kStageWaves * (64 / LPR);
-    constexpr int PPT = DKP / 4;  // float4 pieces per position: a group of PPT consecutive threads
+template <int LPR, int VPL, int NW>
+__device__ __forceinline__ void stage_store(const SeqParams& p, StageSmem<LPR, VPL, NW>& sm, int B, int j,
+                                            const StageRegs<LPR, VPL, NW>& r) {
+    using S = StageShape<LPR, VPL, NW>;
+    constexpr int PPT = S::PPT;  // a position's pieces: a group of PPT consecutive threads
 #pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NKQ; ++m) {
-        const int f = j + kStageThreads * m, tt = f / PPT, col = 4 * (f % PPT);
-        *reinterpret_cast<float4*>(&sm.k[B][tt][col]) = r.k[m];
-        *reinterpret_cast<float4*>(&sm.q[B][tt][col]) = r.q[m];
+    for (int m = 0; m < S::NKQ; ++m) {
+        const int f = j + S::THREADS * m, tt = f / PPT, col = 4 * (f % PPT);
+        if (S::KQ4 % S::THREADS == 0 || f < S::KQ4) {
+            *reinterpret_cast<float4*>(&sm.k[B][tt][col]) = r.k[m];
+            *reinterpret_cast<float4*>(&sm.q[B][tt][col]) = r.q[m];
+        }
         // k.q of position tt, summed over its PPT threads (PPT = 8, 16 or 32)
         float d = r.k[m].x * r.q[m].x + r.k[m].y * r.q[m].y + r.k[m].z * r.q[m].z + r.k[m].w * r.q[m].w;
         d = lane_group_sum<(PPT < 16 ? PPT : 16)>(d);
         if constexpr (PPT == 32) d += __shfl_xor(d, 16, kWave);
-        if ((f % PPT) == 0) sm.gb[B][tt].z = d;
+        if ((f % PPT) == 0 && f < S::KQ4) sm.gb[B][tt].z = d;
     }
 #pragma unroll
-    for (int m = 0; m < StageRegs<LPR>::NV; ++m) {
-        const int f = j + kStageThreads * m, tt = f / (RPB / 4), rr = 4 * (f % (RPB / 4));
-        *reinterpret_cast<float4*>(&sm.v[B][tt][rr]) = r.v[m];
+    for (int m = 0; m < S::NV; ++m) {
+        const int f = j + S::THREADS * m, tt = f / (S::RPB / 4), rr = 4 * (f % (S::RPB / 4));
+        if (S::V4 % S::THREADS == 0 || f < S::V4) *reinterpret_cast<float4*>(&sm.v[B][tt][rr]) = r.v[m];
     }
     if (j < kStageTokens) {
         sm.gb[B][j].x = decay_factor(r.g, p.gate_is_alpha);
@@ -180,19 +213,21 @@ __device__ __forceinline__ void stage_store(const SeqParams& p, StageSmem<LPR>& 
 // Rows i0 .. i0 + RPB - 1 (those below d_v) of sequence `seq`, head h,
 // carried through the whole sequence from the initial state (zero without
 // one): o written for every position, the final state at the end.  Threads
-// j < kStageThreads compute; a workgroup's further threads only take part in
-// its barriers, so every thread of the workgroup must call this.  Every
-// thread loads its share of block b + 1 -- k and q rows of the head, the
-// rows' v, the gates -- into registers while the waves run block b from LDS,
-// then writes it to the other LDS buffer together with k.q of each position
+// j < THREADS compute; a workgroup's further threads only take part in its
+// barriers, so every thread of the workgroup must call this.  Every thread
+// loads its share of block b + 1 -- k and q rows of the head, the rows' v,
+// the gates -- into registers while the waves run block b from LDS, then
+// writes it to the other LDS buffer together with k.q of each position
 // (summed once per workgroup instead of once per row).  A wave then reads
 // each position's k and q from LDS, sums S_i.k and S_i.q over its row's
-// lanes by DPP, and updates its rows.
-template <int LPR, typename T>
-__device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR>& sm, int seq, int h, int i0,
-                                            int j) {
-    constexpr int RPW = 64 / LPR;
-    const bool active = j < kStageThreads;  // uniform per wave
+// lanes by DPP, and updates its rows.  Lane li of a row's group holds
+// columns c*4*LPR + 4*li + e (c < VPL/4, e < 4).
+template <int LPR, typename T, int VPL = 16, int NW = kStageWaves>
+__device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR, VPL, NW>& sm, int seq, int h,
+                                            int i0, int j) {
+    using Sh = StageShape<LPR, VPL, NW>;
+    constexpr int RPW = Sh::RPW;
+    const bool active = j < Sh::THREADS;  // uniform per wave
     const int lane = j & 63, w = j >> 6;
     const int li = lane % LPR;
     const int rr = w * RPW + lane / LPR;  // row within the block of rows
@@ -204,19 +239,20 @@ __device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR>& 
     seq_bounds(p.cu_seqlens, seq, p.seq_len, t0, t1);
     const int nb = (t1 - t0 + kStageTokens - 1) / kStageTokens;
 
-    float s[16];
-    if (p.init && row_ok) {
-        load_slice<LPR, true, float>(p.init + (unit * dv + r) * dk, li, dk, s);
-    } else {
+    float s[VPL];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = 0.f;
+    for (int c = 0; c < VPL / 4; ++c) {
+        const int col = c * 4 * LPR + 4 * li;
+        float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p.init && row_ok && col < dk) f = load4(p.init + (unit * dv + r) * dk + col);
+        s[4 * c] = f.x, s[4 * c + 1] = f.y, s[4 * c + 2] = f.z, s[4 * c + 3] = f.w;
     }
     T* op = static_cast<T*>(p.o);
 
-    StageRegs<LPR> regs;
+    StageRegs<LPR, VPL, NW> regs;
     if (nb > 0 && active) {
-        stage_load<LPR, T>(p, h, i0, t0, min(kStageTokens, t1 - t0), j, regs);
-        stage_store<LPR>(p, sm, 0, j, regs);
+        stage_load<LPR, VPL, NW, T>(p, h, i0, t0, min(kStageTokens, t1 - t0), j, regs);
+        stage_store<LPR, VPL, NW>(p, sm, 0, j, regs);
     }
     __syncthreads();
     T* orow = op + (long)h * dv + r;  // o of position t at orow + t * H * dv
@@ -228,11 +264,12 @@ __device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR>& 
         const bool more = b + 1 < nb;  // uniform
         if (active) {
             if (more)
-                stage_load<LPR, T>(p, h, i0, tb + kStageTokens, min(kStageTokens, t1 - tb - kStageTokens), j, regs);
+                stage_load<LPR, VPL, NW, T>(p, h, i0, tb + kStageTokens, min(kStageTokens, t1 - tb - kStageTokens),
+                                            j, regs);
             for (int tt = 0; tt < len; ++tt) {
-                float kr[16], qr[16];
+                float kr[VPL], qr[VPL];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
+                for (int c = 0; c < VPL / 4; ++c) {
                     const float4 a = *reinterpret_cast<const float4*>(&sm.k[B][tt][c * 4 * LPR + 4 * li]);
                     const float4 e = *reinterpret_cast<const float4*>(&sm.q[B][tt][c * 4 * LPR + 4 * li]);
                     kr[4 * c] = a.x, kr[4 * c + 1] = a.y, kr[4 * c + 2] = a.z, kr[4 * c + 3] = a.w;
@@ -240,21 +277,29 @@ __device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR>& 
                 }
                 const float4 gb = sm.gb[B][tt];  // alpha, beta, k.q
                 const float vi = sm.v[B][tt][rr];
-                const float sk = lane_group_sum<LPR>(dot16(s, kr));
-                const float sq = lane_group_sum<LPR>(dot16(s, qr));
+                const float sk = lane_group_sum<LPR>(dot_lane<VPL>(s, kr));
+                const float sq = lane_group_sum<LPR>(dot_lane<VPL>(s, qr));
                 const float c = gb.y * fmaf(-gb.x, sk, vi);
                 const float oi = fmaf(gb.x, sq, c * gb.z);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) s[e] = fmaf(gb.x, s[e], c * kr[e]);
+                for (int e = 0; e < VPL; ++e) s[e] = fmaf(gb.x, s[e], c * kr[e]);
                 if (li == 0 && row_ok) Elem<T>::store(orow, (long)(tb + tt) * ostride, oi);
             }
             // buffer B ^ 1 was last read in block b - 1, which every wave has
             // left (the barrier below closed it)
-            if (more) stage_store<LPR>(p, sm, B ^ 1, j, regs);
+            if (more) stage_store<LPR, VPL, NW>(p, sm, B ^ 1, j, regs);
         }
         __syncthreads();
     }
-    if (p.fin && row_ok) store_slice<LPR, true>(p.fin + (unit * dv + r) * dk, li, dk, s);
+    if (p.fin && row_ok) {
+#pragma unroll
+        for (int c = 0; c < VPL / 4; ++c) {
+            const int col = c * 4 * LPR + 4 * li;
+            if (col < dk)
+                *reinterpret_cast<float4*>(p.fin + (unit * dv + r) * dk + col) =
+                    make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]);
+        }
+    }
 }
 
 }  // namespace rhz
