@@ -77,6 +77,11 @@ __host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_c
 // three previous inputs from x (or the sequence's initial state before its
 // start), so spans are independent and the grid covers tokens x channels.
 constexpr int kConvSpan = 16;
+// conv_prepare: spans of 16 tokens, and register use bounded for three
+// waves per SIMD (measured 74.4 against 80.0 us at two waves per SIMD, on
+// 16384 tokens x 6144 bf16 channels).
+constexpr int kConvPrepSpan = 16;
+constexpr int kConvPrepWaves = 3;
 constexpr bool kConvNT = true;  // y by non-temporal stores
 constexpr bool kRowNT = true;   // prepare's and RMSNorm's outputs by non-temporal stores
 
@@ -116,14 +121,14 @@ __device__ __forceinline__ int seq_end(const ConvParams& p, int s) {
 // token of the span that lies in a sequence, in token order, by every thread
 // of the block at once (the tokens are the block's, so the calls stay
 // converged across the block).
-template <typename T, bool VEC, typename Emit>
+template <typename T, bool VEC, int SPAN, typename Emit>
 __device__ __forceinline__ void conv_span(const ConvParams& p, int total, int ncb, Emit&& emit) {
     using V = Vec<T, VEC>;
     constexpr int N = V::N;
     const int c = ((blockIdx.x % ncb) * 256 + threadIdx.x) * N;
-    const int t0 = (blockIdx.x / ncb) * kConvSpan;
+    const int t0 = (blockIdx.x / ncb) * SPAN;
     if (c >= p.C || t0 >= total) return;
-    const int t1 = min(t0 + kConvSpan, total);
+    const int t1 = min(t0 + SPAN, total);
     const T* __restrict__ x = static_cast<const T*>(p.x);  // the outputs never overlap x
     const long C = p.C;
     float w[N][4], b[N];
@@ -147,20 +152,20 @@ __device__ __forceinline__ void conv_span(const ConvParams& p, int total, int nc
 
     int s = seq_of(p, t0);
     int s0 = seq_start(p, s), s1 = seq_end(p, s);
-    if (t1 - t0 == kConvSpan && t0 - 3 >= s0 && t1 <= s1) {
+    if (t1 - t0 == SPAN && t0 - 3 >= s0 && t1 <= s1) {
         // A whole span inside one sequence, three tokens or more past its
         // start: the window comes from x and no state is reset or read, so
         // the span is straight-line code with every load issued up front.
         float a[3][N];
-        typename V::Raw ws[3], xs[kConvSpan];
+        typename V::Raw ws[3], xs[SPAN];
 #pragma unroll
         for (int j = 0; j < 3; ++j) ws[j] = V::load_raw(x + (t0 - 3 + j) * C + c);
 #pragma unroll
-        for (int i = 0; i < kConvSpan; ++i) xs[i] = V::load_raw(x + (t0 + i) * C + c);
+        for (int i = 0; i < SPAN; ++i) xs[i] = V::load_raw(x + (t0 + i) * C + c);
 #pragma unroll
         for (int j = 0; j < 3; ++j) V::unpack(ws[j], a[j]);
 #pragma unroll
-        for (int i = 0; i < kConvSpan; ++i) {
+        for (int i = 0; i < SPAN; ++i) {
             float xt[N], yt[N];
             V::unpack(xs[i], xt);
 #pragma unroll
@@ -200,12 +205,12 @@ __device__ __forceinline__ void conv_span(const ConvParams& p, int total, int nc
 #pragma unroll
     for (int j = 0; j < 3; ++j) window(s, s0, t0 - 3 + j, a[j]);
     // every input of the span first, so that its loads overlap
-    typename V::Raw xs[kConvSpan];
+    typename V::Raw xs[SPAN];
 #pragma unroll
-    for (int i = 0; i < kConvSpan; ++i)
+    for (int i = 0; i < SPAN; ++i)
         if (t0 + i < t1) xs[i] = V::load_raw(x + (t0 + i) * C + c);
 #pragma unroll
-    for (int i = 0; i < kConvSpan; ++i) {
+    for (int i = 0; i < SPAN; ++i) {
         const int t = t0 + i;
         if (t >= t1) break;
         while (t >= s1) {  // next sequence (skipping empty ones)
@@ -245,7 +250,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p, int total, in
     using V = Vec<T, VEC>;
     T* __restrict__ y = static_cast<T*>(p.y);
     const long C = p.C;
-    conv_span<T, VEC>(p, total, ncb, [&](int t, int c, const float (&yt)[V::N]) {
+    conv_span<T, VEC, kConvSpan>(p, total, ncb, [&](int t, int c, const float (&yt)[V::N]) {
         V::template store<kConvNT>(y + t * C + c, yt);
     });
 }
@@ -289,7 +294,7 @@ __device__ __forceinline__ float row_sum(float x) {
 }
 
 template <typename T, int G>
-__global__ __launch_bounds__(256) void conv_prepare_kernel(ConvPrepParams p, int total, int ncb) {
+__global__ __launch_bounds__(256, kConvPrepWaves) void conv_prepare_kernel(ConvPrepParams p, int total, int ncb) {
     using V = Vec<T, true>;
     constexpr int N = V::N;
     const int H = p.heads, dk = p.d_k, dv = p.d_v;
@@ -297,7 +302,7 @@ __global__ __launch_bounds__(256) void conv_prepare_kernel(ConvPrepParams p, int
     T* __restrict__ qo = static_cast<T*>(p.q);
     T* __restrict__ ko = static_cast<T*>(p.k);
     T* __restrict__ vo = static_cast<T*>(p.v);
-    conv_span<T, true>(p.conv, total, ncb, [&](int t, int c, const float (&yt)[N]) {
+    conv_span<T, true, kConvPrepSpan>(p.conv, total, ncb, [&](int t, int c, const float (&yt)[N]) {
         if (c >= 2 * qk) {  // v (uniform over the row's lanes)
             V::template store<kConvNT>(vo + (long)t * H * dv + (c - 2 * qk), yt);
             return;
@@ -319,10 +324,10 @@ __global__ __launch_bounds__(256) void conv_prepare_kernel(ConvPrepParams p, int
     // The gates of the block's (token, head) pairs, one pair per thread: the
     // blocks holding q channels cover every head once per span.
     const int cb = (blockIdx.x % ncb) * 256 * N;  // first channel of the block
-    const int t0 = (blockIdx.x / ncb) * kConvSpan;
+    const int t0 = (blockIdx.x / ncb) * kConvPrepSpan;
     if (cb >= qk || t0 >= total) return;
     const int h0 = cb / dk, nh = (min(cb + 256 * N, qk) - cb) / dk;
-    const int nt = min(t0 + kConvSpan, total) - t0;
+    const int nt = min(t0 + kConvPrepSpan, total) - t0;
     for (int i = threadIdx.x; i < nt * nh; i += 256) {
         const int h = h0 + i % nh;
         const long r = (long)(t0 + i / nh) * H + h;
@@ -577,7 +582,7 @@ hipError_t launch_conv_prepare(const rhz_gdr_conv_prepare_args& a, hipStream_t s
     const int g = a.d_k / n;
     const int ncb = (C / n + 255) / 256;
     if (total > 0) {
-        const dim3 grid((unsigned)((long)ncb * ((total + kConvSpan - 1) / kConvSpan)));
+        const dim3 grid((unsigned)((long)ncb * ((total + kConvPrepSpan - 1) / kConvPrepSpan)));
 #define RHZ_CONV_PREP(T, G) hipLaunchKernelGGL((conv_prepare_kernel<T, G>), grid, dim3(256), 0, st, p, total, ncb)
         if (a.dtype == RHZ_F32) {
             switch (g) {
