@@ -98,6 +98,15 @@ constexpr int kStageThreads = kStageWaves * kWave;
 // The dot product of a lane's VPL columns (four partial sums).
 template <int VPL>
 __device__ __forceinline__ float dot_lane(const float (&a)[VPL], const float (&b)[VPL]) {
+    if constexpr (VPL == 8) {
+        float s0 = a[0] * b[0], s1 = a[1] * b[1];
+#pragma unroll
+        for (int e = 2; e < 8; e += 2) {
+            s0 = fmaf(a[e], b[e], s0);
+            s1 = fmaf(a[e + 1], b[e + 1], s1);
+        }
+        return s0 + s1;
+    }
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
     for (int c = 0; c < VPL / 4; ++c) {
@@ -280,7 +289,11 @@ __device__ __forceinline__ void staged_rows(const SeqParams& p, StageSmem<LPR, V
                 const float sk = lane_group_sum<LPR>(dot_lane<VPL>(s, kr));
                 const float sq = lane_group_sum<LPR>(dot_lane<VPL>(s, qr));
                 const float c = gb.y * fmaf(-gb.x, sk, vi);
-                const float oi = fmaf(gb.x, sq, c * gb.z);
+                float oi = fmaf(gb.x, sq, c * gb.z);
+                // o is formed by every lane, ahead of the store's branch, so
+                // that k.q is read with the position's other gates rather
+                // than inside the branch (an LDS wait per position there)
+                asm volatile("" : "+v"(oi));
 #pragma unroll
                 for (int e = 0; e < VPL; ++e) s[e] = fmaf(gb.x, s[e], c * kr[e]);
                 if (li == 0 && row_ok) Elem<T>::store(orow, (long)(tb + tt) * ostride, oi);
