@@ -643,7 +643,7 @@ __device__ __forceinline__ void stage_gates(const ChunkParams& p, Smem<DK>& sm, 
     const float g = s < len && !rst ? graw : 0.f;
     const float beta = s < len ? (PRE ? fast_sigmoid(r.b) : r.b) : 0.f;
     if constexpr (!PRE) {
-        dom.gmax = max3_abs3(dom.gmax, graw + 0.5f, beta - 0.5f);
+        dom.gmax = fmaxf(dom.gmax, fmaxf(graw + 0.5f, fabsf(beta - 0.5f)));
         dom.nan |= __builtin_isunordered(graw, beta) ? 1 : 0;
     }
     if (__builtin_amdgcn_ballot_w64(rst) == 0)
@@ -755,62 +755,81 @@ __device__ __forceinline__ void load_rows(const uint16_t* src, int blk, int n, i
 
 // One 16x16 block (BI, BJ), BJ <= BI, of K K^T (ISQ false) or Q K^T for
 // chunk buffer NB, formed transposed, out^T = K_BJ Y_BI^T, so that lane
-// (n, g) holds out[16 BI + n][16 BJ + 4 g + 0..3].  xk holds the K rows of
-// block BJ, y the rows of block BI of K or Q.  Off-diagonal blocks go to A
-// (beta and decay applied) or P (decay applied) in fp16; the decay is the
-// product of three factors <= 1, exp(G_r - G_{16 BI}) exp(G_{16 BI} -
-// G_{16 BJ + 15}) exp(G_{16 BJ + 15} - G_s).  Diagonal blocks are masked to
-// s < r (A, kept in fp32 for the substitution) or s <= r (P).  The fp16
-// values pass through rng's range watch.  kmax keeps the running maximum of
-// the unmasked products of A's diagonal blocks: it bounds max_r |k_r|^2 from
+// (n, g) holds out[16 BI + n][16 BJ + 4 g + 0..3].  The block's product is
+// 16x16x32 MFMAs over the key columns (kq_mma); load() reads its epilogue
+// factors and store() writes it.  Off-diagonal blocks go to A (beta and
+// decay applied) or P (decay applied) in fp16; the decay is the product of
+// three factors <= 1, exp(G_r - G_{16 BI}) exp(G_{16 BI} - G_{16 BJ + 15})
+// exp(G_{16 BJ + 15} - G_s).  Diagonal blocks are masked to s < r (A, kept
+// in fp32 for the substitution) or s <= r (P).  The fp16 values pass
+// through rng's range watch.  kmax keeps the running maximum of the
+// unmasked products of A's diagonal blocks: it bounds max_r |k_r|^2 from
 // below by the diagonal entries and is bounded by it (|k_r.k_s| <= |k_r||k_s|).
+// A wave forms its several blocks together: every block's factors are read,
+// then the blocks' MFMAs are issued interleaved (independent accumulators),
+// then every block is stored.
 template <int DK, int NB, bool ISQ, int BI, int BJ>
-__device__ __forceinline__ void kq_block(Smem<DK>& sm, const f16x8* xk, const f16x8* y, int l, uint32_t& rng,
-                                         float& kmax) {
-    constexpr int NK = DK / 32;
-    constexpr bool diag = BI == BJ;
-    const int n = l & 15, g = l >> 4;
-    const int r = 16 * BI + n, s0 = 16 * BJ + 4 * g;
-    // Epilogue factors, read before the products.
-    const float br = ISQ ? 1.f : sm.bs[NB][r];
-    const float Gr = sm.gcum[NB][r];
-    const float fr = diag ? 0.f : sm.dst[NB][r] * sm.pf[NB][4 * BI + BJ];
-    const f32x4 es = ld_f32x4(diag ? &sm.gcum[NB][s0] : &sm.den[NB][s0]);
-    const int resets = diag ? __builtin_amdgcn_readfirstlane(sm.resets[NB]) : 0;
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+struct KqBlock {
+    static constexpr bool diag = BI == BJ;
+    float br, Gr, fr;
+    f32x4 es;
+    __device__ __forceinline__ void load(Smem<DK>& sm, int l) {
+        const int n = l & 15, g = l >> 4;
+        const int r = 16 * BI + n, s0 = 16 * BJ + 4 * g;
+        br = ISQ ? 1.f : sm.bs[NB][r];
+        Gr = sm.gcum[NB][r];
+        fr = diag ? 0.f : sm.dst[NB][r] * sm.pf[NB][4 * BI + BJ];
+        es = ld_f32x4(diag ? &sm.gcum[NB][s0] : &sm.den[NB][s0]);
+    }
+    __device__ __forceinline__ void store(Smem<DK>& sm, int l, const f32x4& acc, int resets, uint32_t& rng,
+                                          float& kmax) const {
+        const int n = l & 15, g = l >> 4;
+        const int r = 16 * BI + n, s0 = 16 * BJ + 4 * g;
+        f32x4 x;
+        if constexpr (!diag) {
+            const float f = fr * br;
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) acc = mfma16x32h(xk[ks], y[ks], acc);
-    f32x4 x;
-    if constexpr (!diag) {
-        const float f = fr * br;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) x[v] = acc[v] * f * es[v];
-        const uint2 h = pack_f16x4(x);
-        range_watch(rng, h);
-        *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = h;
-    } else {
-        if constexpr (!ISQ) kmax = max3_raw(max3_raw(kmax, acc[0], acc[1]), acc[2], acc[3]);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int s = s0 + v;
-            const bool keep = ISQ ? (s <= r) : (s < r);
-            x[v] = keep ? acc[v] * br * __expf(Gr - es[v]) : 0.f;
-        }
-        if (resets) {  // only pairs in one segment (no reset in (s, r])
-            const float sr = sm.seg[NB][r];
-            const f32x4 ss = ld_f32x4(&sm.seg[NB][s0]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) x[v] = ss[v] == sr ? x[v] : 0.f;
-        }
-        if constexpr (ISQ) {
+            for (int v = 0; v < 4; ++v) x[v] = acc[v] * f * es[v];
             const uint2 h = pack_f16x4(x);
             range_watch(rng, h);
-            *reinterpret_cast<uint2*>(&sm.p[NB][toff(r, s0)]) = h;
+            *reinterpret_cast<uint2*>(&(ISQ ? sm.p[NB] : sm.a)[toff(r, s0)]) = h;
         } else {
-            *reinterpret_cast<float4*>(&sm.ad[(16 * BI + n) * kLDD + 4 * g]) = make_float4(x[0], x[1], x[2], x[3]);
+            // plain maxima, so that the compiler orders this read of the
+            // accumulators after the MFMAs that write them
+            if constexpr (!ISQ) kmax = fmaxf(kmax, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int s = s0 + v;
+                const bool keep = ISQ ? (s <= r) : (s < r);
+                x[v] = keep ? acc[v] * br * __expf(Gr - es[v]) : 0.f;
+            }
+            if (resets) {  // only pairs in one segment (no reset in (s, r])
+                const float sr = sm.seg[NB][r];
+                const f32x4 ss = ld_f32x4(&sm.seg[NB][s0]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) x[v] = ss[v] == sr ? x[v] : 0.f;
+            }
+            if constexpr (ISQ) {
+                const uint2 h = pack_f16x4(x);
+                range_watch(rng, h);
+                *reinterpret_cast<uint2*>(&sm.p[NB][toff(r, s0)]) = h;
+            } else {
+                *reinterpret_cast<float4*>(&sm.ad[(16 * BI + n) * kLDD + 4 * g]) = make_float4(x[0], x[1], x[2], x[3]);
+            }
         }
     }
+};
+
+// acc[i] = X_i Y_i^T over the key columns for NB blocks at once, the
+// MFMAs of the blocks interleaved.
+template <int DK, int N>
+__device__ __forceinline__ void kq_mma(const f16x8* const (&x)[N], const f16x8* const (&y)[N], f32x4 (&acc)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < DK / 32; ++ks)
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] = mfma16x32h(x[i][ks], y[i][ks], acc[i]);
 }
 
 // a from lane R of each row of 16 lanes (DPP row_newbcast) times t, and the
@@ -925,10 +944,20 @@ __device__ __forceinline__ void prep_wave2(Smem<DK>& sm, int x, int l, int lim, 
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
     uint32_t unused = 0;  // diagonal blocks of A stay fp32
-    kq_block<DK, B, false, 0, 0>(sm, kr[0], kr[0], l, unused, kmax);
-    kq_block<DK, B, false, 1, 1>(sm, kr[1], kr[1], l, unused, kmax);
-    kq_block<DK, B, false, 2, 2>(sm, kr[2], kr[2], l, unused, kmax);
-    kq_block<DK, B, false, 3, 3>(sm, kr[3], kr[3], l, unused, kmax);
+    {
+        KqBlock<DK, B, false, 0, 0> b0;
+        KqBlock<DK, B, false, 1, 1> b1;
+        KqBlock<DK, B, false, 2, 2> b2;
+        KqBlock<DK, B, false, 3, 3> b3;
+        b0.load(sm, l), b1.load(sm, l), b2.load(sm, l), b3.load(sm, l);
+        const int resets = __builtin_amdgcn_readfirstlane(sm.resets[B]);
+        f32x4 acc[4];
+        kq_mma<DK, 4>({kr[0], kr[1], kr[2], kr[3]}, {kr[0], kr[1], kr[2], kr[3]}, acc);
+        b0.store(sm, l, acc[0], resets, unused, kmax);
+        b1.store(sm, l, acc[1], resets, unused, kmax);
+        b2.store(sm, l, acc[2], resets, unused, kmax);
+        b3.store(sm, l, acc[3], resets, unused, kmax);
+    }
     lds_fence();
     t_diag<DK, B>(sm, l);
     signal(&sm.sync.tdiag);
@@ -952,12 +981,23 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
     f16x8 kr[4][NK];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) load_rows<DK>(sm.k[B], blk, n, g, kr[blk]);
-    kq_block<DK, B, false, 1, 0>(sm, kr[0], kr[1], l, rng, unused);
-    kq_block<DK, B, false, 2, 0>(sm, kr[0], kr[2], l, rng, unused);
-    kq_block<DK, B, false, 3, 0>(sm, kr[0], kr[3], l, rng, unused);
-    kq_block<DK, B, false, 2, 1>(sm, kr[1], kr[2], l, rng, unused);
-    kq_block<DK, B, false, 3, 1>(sm, kr[1], kr[3], l, rng, unused);
-    kq_block<DK, B, false, 3, 2>(sm, kr[2], kr[3], l, rng, unused);
+    {
+        KqBlock<DK, B, false, 1, 0> b10;
+        KqBlock<DK, B, false, 2, 0> b20;
+        KqBlock<DK, B, false, 3, 0> b30;
+        KqBlock<DK, B, false, 2, 1> b21;
+        KqBlock<DK, B, false, 3, 1> b31;
+        KqBlock<DK, B, false, 3, 2> b32;
+        b10.load(sm, l), b20.load(sm, l), b30.load(sm, l), b21.load(sm, l), b31.load(sm, l), b32.load(sm, l);
+        f32x4 acc[6];
+        kq_mma<DK, 6>({kr[0], kr[0], kr[0], kr[1], kr[1], kr[2]}, {kr[1], kr[2], kr[3], kr[2], kr[3], kr[3]}, acc);
+        b10.store(sm, l, acc[0], 0, rng, unused);
+        b20.store(sm, l, acc[1], 0, rng, unused);
+        b30.store(sm, l, acc[2], 0, rng, unused);
+        b21.store(sm, l, acc[3], 0, rng, unused);
+        b31.store(sm, l, acc[4], 0, rng, unused);
+        b32.store(sm, l, acc[5], 0, rng, unused);
+    }
     signal(&sm.sync.aoff);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
@@ -974,35 +1014,61 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
     const int n = l & 15, g = l >> 4;
     float unused = 0.f;  // Q K^T: no norm bound
-    f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
+    const int resets = __builtin_amdgcn_readfirstlane(sm.resets[NB]);
     if constexpr (LW == 0) {
+        f16x8 x0[NK], y0[NK], y1[NK];
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 0, n, g, y0);
         load_rows<DK>(sm.q[NB], 1, n, g, y1);
-        kq_block<DK, NB, true, 0, 0>(sm, x0, y0, l, rng, unused);
-        kq_block<DK, NB, true, 1, 0>(sm, x0, y1, l, rng, unused);
+        KqBlock<DK, NB, true, 0, 0> b0;
+        KqBlock<DK, NB, true, 1, 0> b1;
+        b0.load(sm, l), b1.load(sm, l);
+        f32x4 acc[2];
+        kq_mma<DK, 2>({x0, x0}, {y0, y1}, acc);
+        b0.store(sm, l, acc[0], resets, rng, unused);
+        b1.store(sm, l, acc[1], resets, rng, unused);
     } else if constexpr (LW == 1) {
+        f16x8 x0[NK], y0[NK], y1[NK];
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.q[NB], 1, n, g, y0);
         load_rows<DK>(sm.q[NB], 2, n, g, y1);
-        kq_block<DK, NB, true, 1, 1>(sm, x0, y0, l, rng, unused);
-        kq_block<DK, NB, true, 2, 1>(sm, x0, y1, l, rng, unused);
+        KqBlock<DK, NB, true, 1, 1> b0;
+        KqBlock<DK, NB, true, 2, 1> b1;
+        b0.load(sm, l), b1.load(sm, l);
+        f32x4 acc[2];
+        kq_mma<DK, 2>({x0, x0}, {y0, y1}, acc);
+        b0.store(sm, l, acc[0], resets, rng, unused);
+        b1.store(sm, l, acc[1], resets, rng, unused);
     } else if constexpr (LW == 2) {
+        f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 2, n, g, y0);
         load_rows<DK>(sm.q[NB], 3, n, g, y1);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 2, 0>(sm, x0, y0, l, rng, unused);
-        kq_block<DK, NB, true, 3, 0>(sm, x0, y1, l, rng, unused);
-        kq_block<DK, NB, true, 2, 2>(sm, x1, y0, l, rng, unused);
+        KqBlock<DK, NB, true, 2, 0> b0;
+        KqBlock<DK, NB, true, 3, 0> b1;
+        KqBlock<DK, NB, true, 2, 2> b2;
+        b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
+        f32x4 acc[3];
+        kq_mma<DK, 3>({x0, x0, x1}, {y0, y1, y0}, acc);
+        b0.store(sm, l, acc[0], resets, rng, unused);
+        b1.store(sm, l, acc[1], resets, rng, unused);
+        b2.store(sm, l, acc[2], resets, rng, unused);
     } else {
+        f16x8 x0[NK], x1[NK], x2[NK], y0[NK];
         load_rows<DK>(sm.q[NB], 3, n, g, y0);
         load_rows<DK>(sm.k[NB], 1, n, g, x0);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        kq_block<DK, NB, true, 3, 1>(sm, x0, y0, l, rng, unused);
-        kq_block<DK, NB, true, 3, 2>(sm, x1, y0, l, rng, unused);
-        load_rows<DK>(sm.k[NB], 3, n, g, x0);
-        kq_block<DK, NB, true, 3, 3>(sm, x0, y0, l, rng, unused);
+        load_rows<DK>(sm.k[NB], 3, n, g, x2);
+        KqBlock<DK, NB, true, 3, 1> b0;
+        KqBlock<DK, NB, true, 3, 2> b1;
+        KqBlock<DK, NB, true, 3, 3> b2;
+        b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
+        f32x4 acc[3];
+        kq_mma<DK, 3>({x0, x1, x2}, {y0, y0, y0}, acc);
+        b0.store(sm, l, acc[0], resets, rng, unused);
+        b1.store(sm, l, acc[1], resets, rng, unused);
+        b2.store(sm, l, acc[2], resets, rng, unused);
     }
 }
 

@@ -58,20 +58,6 @@ __device__ __forceinline__ float dpp_mov(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
-// max(a, b, c) and max(a, b, |c|) as one v_max3_f32, without the operand
-// canonicalisation that fmaxf brings (for running maxima where a NaN operand
-// may be dropped).
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float max3_abs3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, |%3|" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-
 // Maximum over the 64 lanes of a wave, returned to every lane: DPP within
 // rows of 16 (quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), then the
 // four row maxima through scalar registers.
