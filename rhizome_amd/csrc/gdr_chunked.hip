@@ -392,7 +392,8 @@ struct Sync {
     int tdiag;   // wave 2 (1 per chunk): K K^T diagonal blocks and T's diagonal blocks
     int aoff;    // wave 3 (1 per chunk): A below the diagonal
     int tfull;   // waves 2, 3 (2 per chunk): T complete
-    int pdone;   // loader waves (4 per chunk): P
+    int pdone;   // loader waves 0-2 (3 per chunk): P's first three block rows
+    int pdone3;  // wave 3 (1 per chunk): P's last block row
     int scanned[2];  // scan wave w (1 per chunk): its last read of the chunk's buffers returned
     int rerun;       // nonzero: an input left the fp16 path's domain (set once, read after the loops)
 };
@@ -930,6 +931,9 @@ __device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
     *reinterpret_cast<uint2*>(&tt[toff(16 * I + n, 16 * J + 4 * kg)]) = pack_f16x4(-t);
 }
 
+template <int DK, int NB, int LW>
+__device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng);
+
 // ------------------------------------------------------------ prep roles
 // Wave 2, chunk x (buffer B = x & 1): K K^T's diagonal blocks and T's
 // diagonal blocks, then T_10, T_20, T_30.
@@ -999,6 +1003,11 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
         b32.store(sm, l, acc[5], 0, rng, unused);
     }
     signal(&sm.sync.aoff);
+    // Q K^T's last block row (the gate loader's share of P would put it on
+    // the chunk's critical loop; this wave waits for the diagonal T blocks
+    // here anyway)
+    qk_blocks<DK, B, kGateWave>(sm, l, rng);
+    signal(&sm.sync.pdone3);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
     t_block<DK, B, 2, 1>(sm, l);
@@ -1081,15 +1090,19 @@ __device__ __forceinline__ void prep_loader(const ChunkParams& p, Smem<DK>& sm, 
                                             ChunkIn<DK>& in, uint32_t& rng, GateDomain& dom) {
     // buffer B held chunk x - 2: every reader of it is done (nothing to wait for when x < 2)
     Sync& sy = sm.sync;
-    wait_all<5>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.tdiag, &sy.aoff},
-                {x - 1, x - 1, 4 * (x - 1), x - 1, x - 1});
+    wait_all<6>(p.spin_limit, {&sy.scanned[0], &sy.scanned[1], &sy.pdone, &sy.pdone3, &sy.tdiag, &sy.aoff},
+                {x - 1, x - 1, 3 * (x - 1), x - 1, x - 1, x - 1});
     const int len = min(kChunk, u.te - (u.tb + x * kChunk));
     stage_chunk<DK, B, LW == kGateWave, PRE>(p, sm, u, len, u.i0, lt, in, dom);
     signal(&sm.sync.staged);
     load_chunk_any<DK>(p, u, x + 2, lo, lastc, in);
+    // every loader waits for all four to have staged x, so that none stages
+    // x + 1 first (staged counts 4 per chunk)
     wait_ge(p.spin_limit, &sm.sync.staged, 4 * (x + 1));
-    qk_blocks<DK, B, LW>(sm, lt & 63, rng);
-    signal(&sm.sync.pdone);
+    if constexpr (LW != kGateWave) {  // the gate loader's Q K^T blocks are wave 3's
+        qk_blocks<DK, B, LW>(sm, lt & 63, rng);
+        signal(&sm.sync.pdone);
+    }
 }
 
 template <int DK, int LW, bool PRE>
@@ -1241,7 +1254,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         for (int tb2 = 0; tb2 < 4; ++tb2) OQ[tb2] *= gq[tb2] * fo;
     }
     // ---- U = T Rhat, O^T += U^T P^T, S update.
-    wait_all<2>(p.spin_limit, {&sm.sync.tfull, &sm.sync.pdone}, {2 * (c + 1), 4 * (c + 1)});
+    wait_all<3>(p.spin_limit, {&sm.sync.tfull, &sm.sync.pdone, &sm.sync.pdone3}, {2 * (c + 1), 3 * (c + 1), c + 1});
     {
         const int F1 = st.F + er;
         // T rows (both 32-token halves for rows >= 32), P rows, decays.
@@ -1397,7 +1410,7 @@ __global__ __launch_bounds__(512) void gdr_chunk_kernel(ChunkParams p) {
         base[it % (2 * 64 * kLDT / 8)] = make_uint4(0, 0, 0, 0);
     }
     if (tid == 0) {
-        sm.sync = Sync{0, 0, 0, 0, 0, {0, 0}, 0};
+        sm.sync = Sync{0, 0, 0, 0, 0, 0, {0, 0}, 0};
         if constexpr (!PRE)
             sm.rerun_args = RerunArgs{{p.q, p.k, p.v, p.gate, p.beta, p.cu_seqlens, p.init, p.fin, p.o, p.seq_len,
                                        p.heads, p.d_k, p.d_v, p.gate_is_alpha},

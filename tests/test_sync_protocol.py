@@ -14,19 +14,29 @@ and writes land when the step ends.  It asserts:
   LDS buffer sees the chunk the reader expects.
 
 Roles and their kernel functions:
-  loader L (4 waves)  prep_loader: wait {scanned[0..1] >= x-1, pdone >= 4(x-1),
-                      tdiag >= x-1, aoff >= x-1}, stage K/Q/beta V/gates of x
-                      into buffer x&1, signal staged; wait staged >= 4(x+1),
-                      Q K^T -> P[x&1], signal pdone
+  loader L (4 waves)  prep_loader: wait {scanned[0..1] >= x-1, pdone >= 3(x-1),
+                      pdone3 >= x-1, tdiag >= x-1, aoff >= x-1}, stage
+                      K/Q/beta V/gates of x into buffer x&1, signal staged;
+                      wait staged >= 4(x+1); loaders 0-2 then form Q K^T's
+                      block rows -> P[x&1], signal pdone (the gate loader, 3,
+                      has no Q K^T share, but waits all the same: without
+                      that wait it could stage x+1 before the others staged
+                      x, and staged >= 4(x+1) would then not mean that all
+                      four staged x, the planted mistake
+                      "gate_loader_runs_ahead")
   wave 2              prep_wave2: wait {staged >= 4(x+1), scanned >= x-1,
                       tfull >= 2(x-1)}, K K^T diagonal -> A diag, T diagonal
                       blocks, signal tdiag; wait aoff >= x+1, T blocks, signal tfull
   wave 3              prep_wave3: wait {staged >= 4(x+1), tfull >= 2x}, A below
-                      the diagonal, signal aoff; wait tdiag >= x+1, T blocks,
+                      the diagonal, signal aoff; Q K^T's last block row ->
+                      P[x&1], signal pdone3; wait tdiag >= x+1, T blocks,
                       signal tfull
   scan s (2 waves)    scan_chunk: wait staged >= 4(c+1), read K, Q, beta V,
-                      gates; wait {tfull >= 2(c+1), pdone >= 4(c+1)}, read T,
-                      P, K^T, gates, signal scanned[s]
+                      gates; wait {tfull >= 2(c+1), pdone >= 3(c+1),
+                      pdone3 >= c+1}, read T, P, K^T, gates, signal scanned[s]
+
+P's last block row, formed by wave 3, has a counter of its own (pdone3), so
+that each counter counts one kind of step.
 
 The planted mistakes at the end (each a wait target the kernel does NOT
 have) must be caught, which shows that the model can see a broken protocol.
@@ -43,12 +53,11 @@ def _roles(nch, cnt, rd, wr, mistake=None):
             b = x & 1
 
             def w_stage(x=x):
+                pd = cnt["pdone"] >= 3 * (x - 1) and cnt["pdone3"] >= x - 1
                 if mistake == "loader_ignores_scan":
-                    return x < 2 or (cnt["pdone"] >= 4 * (x - 1) and cnt["tdiag"] >= x - 1
-                                     and cnt["aoff"] >= x - 1)
+                    return x < 2 or (pd and cnt["tdiag"] >= x - 1 and cnt["aoff"] >= x - 1)
                 return x < 2 or (min(cnt["scanned0"], cnt["scanned1"]) >= x - 1
-                                 and cnt["pdone"] >= 4 * (x - 1) and cnt["tdiag"] >= x - 1
-                                 and cnt["aoff"] >= x - 1)
+                                 and pd and cnt["tdiag"] >= x - 1 and cnt["aoff"] >= x - 1)
 
             def e_stage(x=x, b=b):
                 for nm in ("k", "q", "vb", "g"):
@@ -58,7 +67,13 @@ def _roles(nch, cnt, rd, wr, mistake=None):
             steps.append((w_stage, lambda: None, e_stage))
 
             def w_qk(x=x):
+                if mistake == "gate_loader_runs_ahead" and L == 3:
+                    return True
                 return cnt["staged"] >= 4 * (x + 1)
+
+            if L == 3:  # the gate loader has no Q K^T share; it only waits
+                steps.append((w_qk, lambda: None, lambda: None))
+                continue
 
             def s_qk(x=x, b=b):
                 for LL in range(4):
@@ -127,6 +142,18 @@ def _roles(nch, cnt, rd, wr, mistake=None):
 
             steps.append((w1, lambda x=x, b=b: all_k(b, x), e1))
 
+            def s_qk(x=x, b=b):
+                for LL in range(4):
+                    for nm in ("k", "q", "g"):
+                        rd(nm + str(LL), b, x)
+
+            def e_qk(x=x, b=b):
+                s_qk(x, b)
+                wr("p3", b, x)
+                cnt["pdone3"] += 1
+
+            steps.append((lambda: True, s_qk, e_qk))
+
             def w2(x=x):
                 return cnt["tdiag"] >= x + 1
 
@@ -158,8 +185,10 @@ def _roles(nch, cnt, rd, wr, mistake=None):
             steps.append((wA, sA, sA))
 
             def wB(c=c):
-                pd = 4 * (c + 1) if mistake != "scan_ignores_pdone" else 0
-                return cnt["tfull"] >= 2 * (c + 1) and cnt["pdone"] >= pd
+                if mistake == "scan_ignores_pdone":
+                    return cnt["tfull"] >= 2 * (c + 1)
+                return (cnt["tfull"] >= 2 * (c + 1) and cnt["pdone"] >= 3 * (c + 1)
+                        and cnt["pdone3"] >= c + 1)
 
             def sB(c=c, b=b):
                 for nm in ("tdiag", "toff2", "toff3"):
@@ -187,7 +216,7 @@ class ProtocolError(AssertionError):
 
 def simulate(nch, seed, mistake=None):
     rng = random.Random(seed)
-    cnt = dict(staged=0, tdiag=0, aoff=0, tfull=0, pdone=0, scanned0=0, scanned1=0)
+    cnt = dict(staged=0, tdiag=0, aoff=0, tfull=0, pdone=0, pdone3=0, scanned0=0, scanned1=0)
     buf = {}  # (buffer, index) -> chunk whose data it holds
 
     def rd(name, idx, x):
@@ -233,7 +262,7 @@ def test_protocol_no_deadlock_no_stale_read(nch):
 # x-2 only after T of x-2 is complete).  Dropping them is therefore no mistake
 # and none is planted there.
 @pytest.mark.parametrize("mistake", ["loader_ignores_scan", "wave2_ignores_aoff", "wave3_early",
-                                     "scan_ignores_pdone"])
+                                     "scan_ignores_pdone", "gate_loader_runs_ahead"])
 def test_planted_mistakes_are_caught(mistake):
     caught = 0
     for seed in range(300):
