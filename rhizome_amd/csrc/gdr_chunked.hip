@@ -375,7 +375,7 @@ __device__ __forceinline__ void map_block(int bid, int units, int nt, int& unit,
 // instead of workgroup barriers, so that every wave waits only for the data
 // it consumes and the preparing waves run up to one chunk ahead of the scan.
 // Each counter counts (waves x chunks) finished; a wave that finishes a step
-// for chunk x adds 1 after its LDS writes have completed, and a consumer
+// for chunk x adds 1 after its LDS accesses for that step, and a consumer
 // waits until the counter reaches (number of producer waves) * (x + 1).  A
 // shared count is exact only because the producers of one counter cannot
 // drift apart by a chunk (each waits, before its next chunk, for a step that
@@ -406,8 +406,15 @@ struct RerunArgs {
 };
 constexpr int kSpinLimit = 1 << 20;
 
+// Adds 1 to a counter once this wave's earlier LDS accesses are performed.
+// A CU's LDS performs the LDS operations of all its waves in one global
+// order that keeps each wave's issue order, so the add, issued after the
+// step's writes (or its last reads of a buffer), is performed after them; a
+// wave that sees the count and then reads sees those writes (or writes
+// after those reads).  No wait for completion is needed, only that the
+// compiler keeps the program order.
 __device__ __forceinline__ void signal(int* cnt) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are complete
+    asm volatile("" ::: "memory");
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     asm volatile("" ::: "memory");
 }
@@ -1304,9 +1311,9 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         };
         constexpr int kAhead = NJ < 4 ? NJ : 4;
         // The last read of buffer B is issued in S-update step kLastRead
-        // (before the loop when negative); once it has returned the buffer is
-        // free, so the chunk is counted there, ahead of the remaining MFMAs,
-        // the output stores and the state maximum.
+        // (before the loop when negative); the count issued right after it
+        // is performed after it, so the chunk is counted there, ahead of the
+        // remaining MFMAs, the output stores and the state maximum.
         constexpr int kLastRead = NJ - 1 - kAhead;
 #pragma unroll
         for (int jb = 0; jb < kAhead; ++jb) kt_load(jb);
