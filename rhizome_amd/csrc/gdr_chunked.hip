@@ -32,15 +32,18 @@
 // into the other half of double-buffered LDS:
 //   waves 4-7 (loaders): K, Q, beta V and the gates of chunk c into LDS from
 //               registers, chunk c+2 into the same registers (two register
-//               sets alternate), then Q K^T of chunk c;
+//               sets alternate), then (loaders 0-2) Q K^T's blocks
+//               other than wave 3's;
 //   wave 2:     K K^T's diagonal blocks, T's diagonal blocks by forward
 //               substitution, T's blocks (1,0), (2,0), (3,0);
-//   wave 3:     K K^T below the diagonal, T's blocks (3,2), (2,1), (3,1).
+//   wave 3:     K K^T below the diagonal, Q K^T's blocks (3,1), (3,2),
+//               (3,3), T's blocks (3,2), (2,1), (3,1).
 // T = (I + A)^-1 is blocked forward substitution: diagonal blocks by
 // substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.  There is no
 // workgroup barrier in the chunk loop: each role publishes its progress in
-// an LDS counter (incremented by one lane after the wave's LDS writes have
-// completed) and waits, by polling, for the counters it depends on; a
+// an LDS counter (incremented by one lane, issued after the step's LDS
+// accesses, which the LDS performs first) and waits, by polling, for the
+// counters it depends on; a
 // buffer is refilled only after both scan waves have counted the chunk that
 // last used it.  The chunk loop is unrolled by two, so that the
 // double-buffer index is a compile-time constant and every LDS address is a
@@ -1024,7 +1027,8 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
 }
 
 // Q K^T blocks of loader wave LW (0..3) for buffer NB:
-//   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)   LW 3: (3,1) (3,2) (3,3)
+//   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)
+//   LW 3 (formed by wave 3; the gate loader has no share): (3,1) (3,2) (3,3)
 template <int DK, int NB, int LW>
 __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
