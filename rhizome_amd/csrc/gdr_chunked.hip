@@ -943,6 +943,8 @@ __device__ __forceinline__ void t_block(Smem<DK>& sm, int l) {
 
 template <int DK, int NB, int LW>
 __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng);
+template <int DK, int NB>
+__device__ __forceinline__ void qk_blocks_w3(Smem<DK>& sm, int l, uint32_t& rng, const f16x8 (&kr)[4][DK / 32]);
 
 // ------------------------------------------------------------ prep roles
 // Wave 2, chunk x (buffer B = x & 1): K K^T's diagonal blocks and T's
@@ -1015,8 +1017,8 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
     signal(&sm.sync.aoff);
     // Q K^T's last block row (the gate loader's share of P would put it on
     // the chunk's critical loop; this wave waits for the diagonal T blocks
-    // here anyway)
-    qk_blocks<DK, B, kGateWave>(sm, l, rng);
+    // here anyway), with K's rows from the registers above
+    qk_blocks_w3<DK, B>(sm, l, rng, kr);
     signal(&sm.sync.pdone3);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
     t_block<DK, B, 3, 2>(sm, l);
@@ -1026,9 +1028,9 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
     signal(&sm.sync.tfull);
 }
 
-// Q K^T blocks of loader wave LW (0..3) for buffer NB:
+// Q K^T blocks of loader wave LW (0..2) for buffer NB:
 //   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)
-//   LW 3 (formed by wave 3; the gate loader has no share): (3,1) (3,2) (3,3)
+// (wave 3 forms (3,1) (3,2) (3,3), qk_blocks_w3; the gate loader has none).
 template <int DK, int NB, int LW>
 __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
@@ -1059,7 +1061,8 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
         kq_mma<DK, 2>({x0, x0}, {y0, y1}, acc);
         b0.store(sm, l, acc[0], resets, rng, unused);
         b1.store(sm, l, acc[1], resets, rng, unused);
-    } else if constexpr (LW == 2) {
+    } else {
+        static_assert(LW == 2, "loader waves 0-2");
         f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 2, n, g, y0);
@@ -1074,22 +1077,28 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
         b0.store(sm, l, acc[0], resets, rng, unused);
         b1.store(sm, l, acc[1], resets, rng, unused);
         b2.store(sm, l, acc[2], resets, rng, unused);
-    } else {
-        f16x8 x0[NK], x1[NK], x2[NK], y0[NK];
-        load_rows<DK>(sm.q[NB], 3, n, g, y0);
-        load_rows<DK>(sm.k[NB], 1, n, g, x0);
-        load_rows<DK>(sm.k[NB], 2, n, g, x1);
-        load_rows<DK>(sm.k[NB], 3, n, g, x2);
-        KqBlock<DK, NB, true, 3, 1> b0;
-        KqBlock<DK, NB, true, 3, 2> b1;
-        KqBlock<DK, NB, true, 3, 3> b2;
-        b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
-        f32x4 acc[3];
-        kq_mma<DK, 3>({x0, x1, x2}, {y0, y0, y0}, acc);
-        b0.store(sm, l, acc[0], resets, rng, unused);
-        b1.store(sm, l, acc[1], resets, rng, unused);
-        b2.store(sm, l, acc[2], resets, rng, unused);
     }
+}
+
+// Wave 3's Q K^T blocks (3,1) (3,2) (3,3) for buffer NB, K's rows 16..63
+// from the registers of its K K^T step, so that only Q's last 16 rows are read.
+template <int DK, int NB>
+__device__ __forceinline__ void qk_blocks_w3(Smem<DK>& sm, int l, uint32_t& rng, const f16x8 (&kr)[4][DK / 32]) {
+    constexpr int NK = DK / 32;
+    const int n = l & 15, g = l >> 4;
+    float unused = 0.f;  // Q K^T: no norm bound
+    const int resets = __builtin_amdgcn_readfirstlane(sm.resets[NB]);
+    f16x8 y0[NK];
+    load_rows<DK>(sm.q[NB], 3, n, g, y0);
+    KqBlock<DK, NB, true, 3, 1> b0;
+    KqBlock<DK, NB, true, 3, 2> b1;
+    KqBlock<DK, NB, true, 3, 3> b2;
+    b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
+    f32x4 acc[3];
+    kq_mma<DK, 3>({kr[1], kr[2], kr[3]}, {y0, y0, y0}, acc);
+    b0.store(sm, l, acc[0], resets, rng, unused);
+    b1.store(sm, l, acc[1], resets, rng, unused);
+    b2.store(sm, l, acc[2], resets, rng, unused);
 }
 
 // Loader wave LW, chunk x (buffer B = x & 1): stage x from registers, load
