@@ -36,8 +36,8 @@
 //               other than wave 3's;
 //   wave 2:     K K^T's diagonal blocks, T's diagonal blocks by forward
 //               substitution, T's blocks (1,0), (2,0), (3,0);
-//   wave 3:     K K^T below the diagonal, Q K^T's blocks (3,1), (3,2),
-//               (3,3), T's blocks (3,2), (2,1), (3,1).
+//   wave 3:     K K^T below the diagonal, Q K^T's last block row, T's
+//               blocks (3,2), (2,1), (3,1).
 // T = (I + A)^-1 is blocked forward substitution: diagonal blocks by
 // substitution, then T_ij = -T_ii sum_m A_im T_mj on MFMA.  There is no
 // workgroup barrier in the chunk loop: each role publishes its progress in
@@ -1017,7 +1017,7 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
     signal(&sm.sync.aoff);
     // Q K^T's last block row (the gate loader's share of P would put it on
     // the chunk's critical loop; this wave waits for the diagonal T blocks
-    // here anyway), with K's rows from the registers above
+    // here anyway), with K from the registers above
     qk_blocks_w3<DK, B>(sm, l, rng, kr);
     signal(&sm.sync.pdone3);
     wait_ge(lim, &sm.sync.tdiag, x + 1);
@@ -1029,8 +1029,8 @@ __device__ __forceinline__ void prep_wave3(Smem<DK>& sm, int x, int l, int lim, 
 }
 
 // Q K^T blocks of loader wave LW (0..2) for buffer NB:
-//   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (3,0) (2,2)
-// (wave 3 forms (3,1) (3,2) (3,3), qk_blocks_w3; the gate loader has none).
+//   LW 0: (0,0) (1,0)   LW 1: (1,1) (2,1)   LW 2: (2,0) (2,2)
+// (wave 3 forms the last block row, qk_blocks_w3; the gate loader has none).
 template <int DK, int NB, int LW>
 __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
     constexpr int NK = DK / 32;
@@ -1063,25 +1063,23 @@ __device__ __forceinline__ void qk_blocks(Smem<DK>& sm, int l, uint32_t& rng) {
         b1.store(sm, l, acc[1], resets, rng, unused);
     } else {
         static_assert(LW == 2, "loader waves 0-2");
-        f16x8 x0[NK], x1[NK], y0[NK], y1[NK];
+        f16x8 x0[NK], x1[NK], y0[NK];
         load_rows<DK>(sm.k[NB], 0, n, g, x0);
         load_rows<DK>(sm.q[NB], 2, n, g, y0);
-        load_rows<DK>(sm.q[NB], 3, n, g, y1);
         load_rows<DK>(sm.k[NB], 2, n, g, x1);
         KqBlock<DK, NB, true, 2, 0> b0;
-        KqBlock<DK, NB, true, 3, 0> b1;
-        KqBlock<DK, NB, true, 2, 2> b2;
-        b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
-        f32x4 acc[3];
-        kq_mma<DK, 3>({x0, x0, x1}, {y0, y1, y0}, acc);
+        KqBlock<DK, NB, true, 2, 2> b1;
+        b0.load(sm, l), b1.load(sm, l);
+        f32x4 acc[2];
+        kq_mma<DK, 2>({x0, x1}, {y0, y0}, acc);
         b0.store(sm, l, acc[0], resets, rng, unused);
         b1.store(sm, l, acc[1], resets, rng, unused);
-        b2.store(sm, l, acc[2], resets, rng, unused);
     }
 }
 
-// Wave 3's Q K^T blocks (3,1) (3,2) (3,3) for buffer NB, K's rows 16..63
-// from the registers of its K K^T step, so that only Q's last 16 rows are read.
+// Wave 3's Q K^T blocks (3,0) .. (3,3), the last block row, for buffer NB,
+// K from the registers of its K K^T step, so that only Q's last 16 rows are
+// read.
 template <int DK, int NB>
 __device__ __forceinline__ void qk_blocks_w3(Smem<DK>& sm, int l, uint32_t& rng, const f16x8 (&kr)[4][DK / 32]) {
     constexpr int NK = DK / 32;
@@ -1090,15 +1088,17 @@ __device__ __forceinline__ void qk_blocks_w3(Smem<DK>& sm, int l, uint32_t& rng,
     const int resets = __builtin_amdgcn_readfirstlane(sm.resets[NB]);
     f16x8 y0[NK];
     load_rows<DK>(sm.q[NB], 3, n, g, y0);
-    KqBlock<DK, NB, true, 3, 1> b0;
-    KqBlock<DK, NB, true, 3, 2> b1;
-    KqBlock<DK, NB, true, 3, 3> b2;
-    b0.load(sm, l), b1.load(sm, l), b2.load(sm, l);
-    f32x4 acc[3];
-    kq_mma<DK, 3>({kr[1], kr[2], kr[3]}, {y0, y0, y0}, acc);
+    KqBlock<DK, NB, true, 3, 0> b0;
+    KqBlock<DK, NB, true, 3, 1> b1;
+    KqBlock<DK, NB, true, 3, 2> b2;
+    KqBlock<DK, NB, true, 3, 3> b3;
+    b0.load(sm, l), b1.load(sm, l), b2.load(sm, l), b3.load(sm, l);
+    f32x4 acc[4];
+    kq_mma<DK, 4>({kr[0], kr[1], kr[2], kr[3]}, {y0, y0, y0, y0}, acc);
     b0.store(sm, l, acc[0], resets, rng, unused);
     b1.store(sm, l, acc[1], resets, rng, unused);
     b2.store(sm, l, acc[2], resets, rng, unused);
+    b3.store(sm, l, acc[3], resets, rng, unused);
 }
 
 // Loader wave LW, chunk x (buffer B = x & 1): stage x from registers, load
