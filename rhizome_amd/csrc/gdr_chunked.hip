@@ -328,6 +328,22 @@ __device__ __forceinline__ int rescale_shift(float m, int lo, int hi, int target
     return min(max(F + s, -kMaxStateExp), kMaxStateExp) - F;
 }
 
+constexpr float pow2f(int e) { return e >= 0 ? float(1ull << e) : 1.f / float(1ull << -e); }
+
+// rescale_shift of the wave maximum of the lanes' maxima loc (each >= 0,
+// never NaN).  The wave maximum m has floor(log2 m) in [LO, HI) exactly when
+// no lane reaches 2^HI and some lane reaches 2^LO, and m is 0 when no lane
+// is above 0, so the common no-shift case is decided by three ballots; the
+// maximum itself is formed only when a shift follows.
+template <int LO, int HI, int TARGET>
+__device__ __forceinline__ int rescale_shift_lanes(float loc, int F) {
+    const bool over = __builtin_amdgcn_ballot_w64(loc >= pow2f(HI)) != 0;
+    const bool inside = __builtin_amdgcn_ballot_w64(loc >= pow2f(LO)) != 0;
+    const bool zero = __builtin_amdgcn_ballot_w64(loc > 0.f) == 0;
+    if (zero || (inside && !over)) return 0;
+    return rescale_shift(wave_max(loc), LO, HI, TARGET, F);
+}
+
 // ------------------------------------------------------------ varlen setup
 #ifndef RHZ_CHUNKED_PROLOGUE_TU  // launched by the plain unit's host code only
 // Longest-first order of the packed sequences (ties by index), so the
@@ -1152,7 +1168,7 @@ template <int DK>
 struct ScanState {
     f32x4 S[DK / 16];  // S[jb][v] = Stilde[i][tok(jb, 4g + v)],  S = Stilde 2^F
     int F;
-    float smax;
+    float smax;  // this lane's maximum of |Stilde|
 };
 
 template <int DK>
@@ -1162,7 +1178,7 @@ __device__ __forceinline__ float state_max(const ScanState<DK>& st) {
     for (int jb = 0; jb < DK / 16; ++jb)
 #pragma unroll
         for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(st.S[jb][v]));
-    return wave_max(m);
+    return m;
 }
 
 // Chunk c of a scan wave (w = 0, 1) on buffer B = c & 1.
@@ -1188,7 +1204,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
         for (int bk = 0; bk < 4; ++bk)
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks) kx[bk][ks] = ld_f16x8(&sm.k[B][KQ<DK>::off(tok(bk, n), 32 * ks + 8 * g)]);
-        const int es = rescale_shift(st.smax, -12, 14, 13, st.F);
+        const int es = rescale_shift_lanes<-12, 14, 13>(st.smax, st.F);
         if (es != 0) {
             const float f = exp2i(-es);
 #pragma unroll
@@ -1258,8 +1274,7 @@ __device__ __forceinline__ void scan_chunk(const ChunkParams& p, Smem<DK>& sm, c
                     rmax = fmaxf(rmax, fabsf(r));
                 }
         }
-        rmax = wave_max(rmax);
-        er = rescale_shift(rmax, -6, 8, 7, st.F);
+        er = rescale_shift_lanes<-6, 8, 7>(rmax, st.F);
         if (er == 0) {
             Br[0] = pack8(XK[0], XK[1]);
             Br[1] = pack8(XK[2], XK[3]);
