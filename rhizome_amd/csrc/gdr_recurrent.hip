@@ -323,11 +323,18 @@ hipError_t decode_pick_lpr(const StepParams& sp, int units, int dk, int dv, hipS
     }
 }
 
+// The multistep launch reserves LDS that the kernel does not use, so that at
+// most two workgroups (eight waves) share a CU's 160 KiB: the snapshot writes
+// then stream from fewer places at once.  B=256 H=16 d=128, 8 positions:
+// 459 us at two workgroups per CU against 480 us at the five that the
+// registers allow, 483 us at four, 495 us at three and 592 us at one.
+constexpr unsigned kMultistepLdsReserve = 64u * 1024u;
+
 template <int LPR, int P, bool VEC, typename T>
 hipError_t multistep_go(const MultiParams& mp, int units, int dv, hipStream_t st) {
     constexpr int RPP = 256 / LPR;
     dim3 grid(units, (dv + P * RPP - 1) / (P * RPP));
-    hipLaunchKernelGGL((gdr_multistep_kernel<LPR, P, VEC, T>), grid, dim3(256), 0, st, mp);
+    hipLaunchKernelGGL((gdr_multistep_kernel<LPR, P, VEC, T>), grid, dim3(256), kMultistepLdsReserve, st, mp);
     return hipGetLastError();
 }
 
